@@ -1,0 +1,150 @@
+/*
+ * wh_sample.h -- C ABI of the MI355X (gfx950) token-selection library
+ * (libwh_sample.so).  Plain pointers and sizes only; every pointer named
+ * "device" is HIP device memory; `stream` is a hipStream_t (NULL = the
+ * default stream).  All entry points are asynchronous and stream ordered:
+ * they validate host-side arguments, enqueue kernels and return; nothing
+ * blocks on the device.  Status: 0 on success, a negative WH_E* code on
+ * failure, with a message from wh_last_error() (thread local).
+ *
+ * The reference exposes this path as Python function objects over MLX arrays,
+ * with no FFI; each entry point below replaces one of them:
+ *
+ *   wh_sample               mlx_lm make_sampler(temp, top_p, top_k, min_p)
+ *                           + make_logits_processors(...), as called at
+ *                           runtime/deepseek_v4_ssd/generation.py:1279-1293 and
+ *                           driven per token by mlx_lm generate_step
+ *                           (generation.py:1465-1475); chain WH_CHAIN_WHALLM is
+ *                           sampling_logprobs + _sample
+ *                           (runtime/deepseek_v4_ssd/dspark.py:358-375, 901-904),
+ *                           with penalties first as in qwen4_exp.py:949-958.
+ *   wh_apply_penalties      the processors returned by make_logits_processors
+ *                           (generation.py:1286-1293), applied in place.
+ *   wh_verify_logprobs      _verify(draft, target_logprobs, temperature)
+ *                           (runtime/deepseek_v4_ssd/dspark.py:857-898).
+ *   wh_verify_fused         _verify fused with the target rows'
+ *                           sampling_logprobs(logits, T, top_p=1)
+ *                           (dspark.py:663-670): target logits in, draft
+ *                           probabilities q in.
+ *
+ * Random numbers: the reference draws from MLX's global PRNG
+ * (mx.random.categorical / uniform, dspark.py:329, 884, 904).  This library
+ * has no RNG: callers pass one uniform in [0,1) per draw, and the draw is the
+ * inverse CDF in vocabulary order over fixed-point weights.
+ */
+#ifndef WH_SAMPLE_H
+#define WH_SAMPLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WH_OK 0
+#define WH_EINVAL -1   /* invalid argument (the reference raises ValueError) */
+#define WH_EHIP -2     /* a HIP runtime call failed */
+#define WH_ELIMIT -3   /* a documented size limit was exceeded */
+
+#define WH_DTYPE_F32 0
+#define WH_DTYPE_BF16 1
+
+/* Filter order.  MLX: mlx_lm make_sampler -- top_k -> top_p -> min_p on the
+ * T=1 logprobs, then categorical(logprobs * (1/T)).  WHALLM: Whallm
+ * sampling_logprobs -- top_p -> min_p -> top_k, then logprobs / max(T, 1e-5),
+ * renormalised. */
+#define WH_CHAIN_MLX 0
+#define WH_CHAIN_WHALLM 1
+
+#define WH_OUT_LOGPROBS 0
+#define WH_OUT_MASKED 1
+
+#define WH_MAX_VOCAB 262144      /* V <= 2^18 keeps fixed-point sums below 2^62 */
+#define WH_MAX_WINDOW 4096       /* penalty window entries per row */
+
+typedef struct wh_sample_args {
+  const void* logits;        /* device, B rows of V values (dtype), row stride in elements */
+  int32_t dtype;             /* WH_DTYPE_F32 or WH_DTYPE_BF16 (widened exactly to float32) */
+  int32_t B;
+  int32_t V;
+  int32_t chain;             /* WH_CHAIN_MLX or WH_CHAIN_WHALLM */
+  int64_t row_stride;
+
+  const int32_t* history;    /* device, nullable: B rows of token ids, stride history_stride */
+  int64_t history_stride;
+  const int32_t* history_len;/* device, [B]; required with history */
+
+  const float* uniforms;     /* device, [B] in [0,1); nullable only when tokens is NULL */
+
+  float temperature;         /* scalar parameters, overridden per row where the */
+  float top_p;               /* matching *_rows pointer is non-NULL            */
+  float min_p;
+  int32_t top_k;
+  const float* temperature_rows; /* device, nullable */
+  const float* top_p_rows;       /* device, nullable */
+  const float* min_p_rows;       /* device, nullable */
+  const int32_t* top_k_rows;     /* device, nullable; k >= V is a no-op */
+
+  float repetition_penalty;  /* 0 = processor absent (1.0 is a no-op) */
+  float presence_penalty;    /* 0 = absent */
+  float frequency_penalty;   /* 0 = absent */
+  int32_t repetition_context;/* window of the last N history ids; 0 = whole history */
+  int32_t presence_context;
+  int32_t frequency_context;
+
+  int32_t* tokens;           /* device, [B] out; nullable when only logprobs_out is wanted */
+  int32_t* kept_count;       /* device, [B] out, nullable: size of the kept set */
+  float* logprobs_out;       /* device, [B, V] out, nullable; see out_mode */
+  int32_t out_mode;          /* WH_OUT_LOGPROBS: sampling_logprobs row (WHALLM chain only);
+                                WH_OUT_MASKED: the (penalised) input row with filtered-out
+                                entries set to -inf, no temperature (mlx_lm apply_top_k /
+                                apply_top_p / apply_min_p) */
+  int32_t reserved;
+  void* workspace;           /* device, wh_sample_workspace_bytes(...) bytes */
+  size_t workspace_bytes;
+} wh_sample_args;
+
+/* Workspace needed by wh_sample for B rows of V entries. */
+size_t wh_sample_workspace_bytes(int32_t B, int32_t V);
+int wh_sample(const wh_sample_args* args, void* stream);
+
+/* Penalty processors only, in place on float32 or bf16 logits (bf16 results
+ * are rounded to nearest even).  Uses the history/penalty fields of args. */
+int wh_apply_penalties(const wh_sample_args* args, void* stream);
+
+typedef struct wh_verify_args {
+  int32_t B;
+  int32_t n;                 /* draft length; target has n+1 rows per batch entry */
+  int32_t V;
+  float temperature;
+  const float* target;       /* device, [B, n+1, V]: logprob rows (wh_verify_logprobs)
+                                or raw logits (wh_verify_fused) */
+  const float* draft;        /* device, [B, n, V]: logprob rows (wh_verify_logprobs)
+                                or probabilities q (wh_verify_fused) */
+  const int32_t* draft_tokens; /* device, [B, n] */
+  const float* uniforms;     /* device, [B, n+1]: [:, j<n] accept tests, [:, n] final draw */
+  int32_t* accepted;         /* device, [B] out */
+  int32_t* token;            /* device, [B] out */
+  float* row_out;            /* device, [B, V] out, nullable (logprob form only) */
+  void* workspace;           /* device, wh_verify_workspace_bytes(...) bytes */
+  size_t workspace_bytes;
+} wh_verify_args;
+
+size_t wh_verify_workspace_bytes(int32_t B, int32_t n, int32_t V);
+int wh_verify_logprobs(const wh_verify_args* args, void* stream);
+int wh_verify_fused(const wh_verify_args* args, void* stream);
+
+/* The contract exponential on device (floor(2^44 exp(d)) for d <= 0), for
+ * bit-exactness tests against the CPU oracle. */
+int wh_exp_fix44(const float* d, uint64_t* out, int64_t n, void* stream);
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* wh_last_error(void);
+/* Library version string. */
+const char* wh_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

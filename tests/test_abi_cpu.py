@@ -1,0 +1,125 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point that
+include/wh_sample.h declares, its structs match the ctypes mirror, and
+host-side argument validation rejects what the reference rejects -- all
+without touching a GPU (invalid calls return before any HIP call)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "wh_sample.h")
+
+
+@pytest.fixture(scope="module")
+def L():
+    from whallm_amd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        from whallm_amd import build
+
+        build.build()
+    return _lib
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\*?\s+\*?(wh_\w+)\s*\(", src, re.M)))
+
+
+def test_library_exports_every_declared_symbol(L):
+    names = declared_functions()
+    assert len(names) >= 8
+    lib = L.lib()
+    for n in names:
+        assert hasattr(lib, n), n
+    out = subprocess.run(["nm", "-D", "--defined-only", L.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (wh_\w+)", out))
+    assert set(names) <= exported
+
+
+def test_struct_layouts_match_ctypes(L, tmp_path):
+    prog = tmp_path / "layout.c"
+    prog.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "wh_sample.h"\n'
+        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(wh_sample_args),"
+        " offsetof(wh_sample_args, uniforms), offsetof(wh_sample_args, top_k_rows),"
+        " offsetof(wh_sample_args, out_mode), offsetof(wh_sample_args, workspace_bytes),"
+        " sizeof(wh_verify_args), offsetof(wh_verify_args, row_out)); return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(prog), "-o", str(exe)], check=True)
+    got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()))
+    S, Vr = L.SampleArgs, L.VerifyArgs
+    want = [ctypes.sizeof(S), S.uniforms.offset, S.top_k_rows.offset, S.out_mode.offset, S.workspace_bytes.offset,
+            ctypes.sizeof(Vr), Vr.row_out.offset]
+    assert got == want
+
+
+def _args(L, **kw):
+    a = L.SampleArgs()
+    a.logits = 1 << 20  # never dereferenced: validation fails first
+    a.dtype = L.DTYPE_F32
+    a.B = 1
+    a.V = 100
+    a.row_stride = 100
+    a.temperature = 1.0
+    a.top_p = 1.0
+    a.chain = L.CHAIN_MLX
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(dtype=7), "dtype"),
+    (dict(V=0), "V must be"),
+    (dict(V=300000, row_stride=300000), "V must be"),
+    (dict(row_stride=50), "row_stride"),
+    (dict(min_p=1.5), "min_p"),
+    (dict(temperature=-1.0), "temperature"),
+    (dict(top_k=100), "top_k"),                      # chain mlx: k must be < V (mlx_lm apply_top_k)
+    (dict(repetition_penalty=-1.0), "penalty"),
+    (dict(chain=5), "chain"),
+    (dict(out_mode=3), "out_mode"),
+])
+def test_host_validation_rejects_bad_arguments(L, kw, needle):
+    a = _args(L, **kw)
+    rc = L.lib().wh_sample(ctypes.byref(a), None)
+    assert rc in (L.WH_EINVAL, L.WH_ELIMIT)
+    assert needle in L.lib().wh_last_error().decode()
+
+
+def test_penalty_window_limit(L):
+    a = _args(L, presence_penalty=0.5, history=1 << 20, history_len=1 << 20, history_stride=8192, presence_context=0)
+    assert L.lib().wh_sample(ctypes.byref(a), None) == L.WH_ELIMIT
+    assert "WH_MAX_WINDOW" in L.lib().wh_last_error().decode()
+
+
+def test_verify_validation(L):
+    a = L.VerifyArgs()
+    a.B, a.n, a.V = 1, 2, 0
+    assert L.lib().wh_verify_logprobs(ctypes.byref(a), None) == L.WH_ELIMIT
+    a.V = 10
+    a.temperature = 1.0
+    a.target = 1 << 20
+    a.accepted = 1 << 20
+    a.token = 1 << 20
+    a.draft_tokens = 1 << 20
+    assert L.lib().wh_verify_logprobs(ctypes.byref(a), None) == L.WH_EINVAL  # draft rows missing at T > 0
+    assert L.lib().wh_verify_fused(ctypes.byref(a), None) == L.WH_EINVAL
+
+
+def test_python_mirror_validation_without_gpu():
+    from whallm_amd import sample_utils as su
+
+    with pytest.raises(ValueError):
+        su.make_sampler(temp=1.0, min_p=2.0)
+    with pytest.raises(ValueError):
+        su.make_repetition_penalty(-0.5)
+    with pytest.raises(NotImplementedError):
+        su.make_logits_processors(logit_bias={1: 2.0})
+    procs = su.make_logits_processors(repetition_penalty=1.1, presence_penalty=0.5, frequency_penalty=0.2)
+    assert [p.kind for p in procs] == ["repetition", "presence", "frequency"]
+    assert su.make_logits_processors() == []

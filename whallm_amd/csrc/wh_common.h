@@ -1,0 +1,168 @@
+// wh_common.h -- device helpers shared by the gfx950 token-selection kernels.
+//
+// Everything here is written for CDNA4 wave64: reductions use 64-lane
+// cross-lane shuffles and one LDS slot per wave.  Arithmetic that decides a
+// token is either IEEE float32 in a fixed operation order (compiled with
+// -ffp-contract=off, so no multiply-add is fused behind our back), or
+// integer fixed point (sums are associative, so any parallel order gives the
+// same bits as the CPU oracle).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define WH_WAVE 64
+
+namespace wh {
+
+typedef unsigned __int128 u128;
+
+// --------------------------------------------------------------------------
+// Contract exponential: floor(2^44 * 2^f * 2^n) with t = fl(d * log2 e) = n+f.
+// p(f) ~ 2^f on [0,1] is a degree-6 minimax polynomial (coefficients fitted
+// for this library; float32 Horner error <= 0.55 ulp).  Inputs d <= 0;
+// t <= -45 and -inf give 0.
+// --------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t exp_fix44(float d) {
+  const float L = 0x1.715476p+0f;
+  float t = d * L;
+  if (!(t > -45.0f)) return 0;
+  if (t > 0.0f) t = 0.0f;
+  float n = floorf(t);
+  float f = t - n;
+  float p = 0x1.c5417ap-13f;
+  p = fmaf(p, f, 0x1.46d64cp-10f);
+  p = fmaf(p, f, 0x1.3d0b92p-7f);
+  p = fmaf(p, f, 0x1.c68912p-5f);
+  p = fmaf(p, f, 0x1.ebfd58p-3f);
+  p = fmaf(p, f, 0x1.62e42cp-1f);
+  p = fmaf(p, f, 1.0f);
+  uint32_t mant = (uint32_t)(p * 8388608.0f);
+  int sh = (int)n + 21;
+  return sh >= 0 ? ((uint64_t)mant << sh) : (uint64_t)(mant >> (-sh));
+}
+
+// float32 mantissa/exponent split: x = M * 2^(e - 24), M a 24-bit integer.
+__device__ __forceinline__ uint64_t mant24(float x, int* e) {
+  float fr = frexpf(x, e);
+  return (uint64_t)ldexpf(fr, 24);
+}
+
+// floor(theta * Z) for float32 theta in [0,1), Z < 2^62 (exact).
+__device__ __forceinline__ uint64_t floor_theta_z(float theta, uint64_t Z) {
+  if (!(theta > 0.0f)) return 0;
+  if (theta > 1.0f) theta = 1.0f;
+  int e;
+  uint64_t M = mant24(theta, &e);
+  int s = 24 - e;
+  u128 prod = (u128)M * (u128)Z;
+  return s >= 128 ? 0 : (uint64_t)(prod >> s);
+}
+
+// u in [0,1) -> floor(u * 2^32), clamped; NaN and negatives give 0.
+__device__ __forceinline__ uint64_t u32_fix(float u) {
+  if (!(u > 0.0f)) return 0;
+  if (u >= 1.0f) return 0xFFFFFFFFull;
+  return (uint64_t)(u * 4294967296.0f);
+}
+
+// Draw target inside a total weight: floor(U * total / 2^32).
+__device__ __forceinline__ uint64_t draw_target(float u, uint64_t total) {
+  return (uint64_t)(((u128)u32_fix(u) * (u128)total) >> 32);
+}
+
+// Monotone 32-bit key of a float (larger value -> larger key); callers map
+// -0 to +0 first so equal floats have equal keys.
+__device__ __forceinline__ uint32_t fkey(float v) {
+  uint32_t u = __float_as_uint(v);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+  return __uint_as_float(u);
+}
+
+// Composite orders over (value, id), larger = earlier:
+//   order A (top-k): value desc, id asc;  order P (top-p): value desc, id desc.
+__device__ __forceinline__ uint64_t comp_a(uint32_t key, int id) {
+  return ((uint64_t)key << 18) | (uint64_t)(0x3FFFF - id);
+}
+__device__ __forceinline__ uint64_t comp_p(uint32_t key, int id) {
+  return ((uint64_t)key << 18) | (uint64_t)id;
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// --------------------------------------------------------------------------
+// Wave / block reductions (blockDim.x a multiple of 64, <= 1024).
+// --------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WH_WAVE));
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WH_WAVE);
+  return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, WH_WAVE));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WH_WAVE);
+  return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WH_WAVE);
+  return v;
+}
+
+// Reductions across the block through a 16-slot LDS scratch (one per wave).
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, T* scratch, Op op, T ident) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, WH_WAVE));
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  T r = ident;
+  for (int i = 0; i < nw; ++i) r = op(r, scratch[i]);
+  return r;
+}
+
+struct OpMaxF { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct OpMinI { __device__ int operator()(int a, int b) const { return min(a, b); } };
+struct OpSumI { __device__ int operator()(int a, int b) const { return a + b; } };
+struct OpSumU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a + b; } };
+struct OpSumF64 { __device__ double operator()(double a, double b) const { return a + b; } };
+struct OpMaxU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
+
+// Exclusive prefix sum of u64 across the block (thread order); returns the
+// exclusive prefix and writes the block total.
+__device__ __forceinline__ uint64_t block_exclusive_scan_u64(uint64_t v, uint64_t* scratch, uint64_t* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  uint64_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    uint64_t y = __shfl_up(x, o, WH_WAVE);
+    if (lane >= o) x += y;
+  }
+  __syncthreads();
+  if (lane == 63) scratch[w] = x;
+  __syncthreads();
+  uint64_t before = 0, tot = 0;
+  for (int i = 0; i < nw; ++i) {
+    uint64_t s = scratch[i];
+    if (i < w) before += s;
+    tot += s;
+  }
+  *total = tot;
+  return before + x - v;
+}
+
+}  // namespace wh
