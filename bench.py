@@ -1,0 +1,204 @@
+"""Benchmark: fused decode-time token selection on one MI355X.
+
+Workload (the headline configuration): B=64 rows, V=151,936 bf16 logits
+~N(0, 3^2), 2,048 Zipf(1.1) history ids per row, presence 0.5 + frequency
+0.3 over the whole history, T 1.0, top-p 0.9, min-p 0.05, mlx_lm filter
+order (top-k -> top-p -> min-p), one uniform per row.  A step is one
+wh_sample call on one batch; 16 distinct input sets (>256 MB) rotate so the
+logits come from HBM rather than the 256 MB Infinity Cache.
+
+Prints one JSON line: rows/s (whole job, inputs resident in HBM), the
+dominant kernel's roofline (algorithmic bytes / average kernel time measured
+with HIP events on the launch stream), and the CPU baseline (the oracle's
+float32 replay of the reference op order, timed on this host's cores).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2]
+    python bench.py --copy-calibration   # plain 256 MiB copies, for PMC scaling
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "sampled rows/sec + % of HBM peak, top-k/top-p sampling at B=64, V=151,936"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 4, 5])
+    ap.add_argument("--sets", type=int, default=16)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
+    return ap.parse_args()
+
+
+def copy_calibration(steps: int):
+    import torch
+
+    n = 256 << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n, "launches": steps}))
+
+
+def make_sets(w, nsets, dev):
+    """Input set 0 is the seeded workload itself; sets 1.. are fresh draws of
+    the same distributions generated on the device."""
+    import torch
+
+    from whallm_amd import synth
+
+    sets = []
+    for s in range(nsets):
+        if s == 0:
+            if w.dtype == "bf16":
+                x = torch.from_numpy(w.logits_bits.view(np.int16)).to(dev).view(torch.bfloat16)
+            else:
+                x = torch.from_numpy(w.logits_f32).to(dev)
+            h = None if w.history is None else torch.from_numpy(w.history).to(dev)
+        else:
+            g = torch.Generator(device=dev)
+            g.manual_seed(1000 + s)
+            base = torch.randn(w.B, w.V, device=dev, generator=g)
+            if w.name.startswith("mtp"):
+                x = (torch.round(base * 2.0 / 0.125) * 0.125)
+            elif w.name.startswith("top-k"):
+                x = torch.distributions.StudentT(3.0).sample((w.B, w.V)).to(dev) * 3.0
+            else:
+                x = base * float(np.std(w.logits_f32[0]))
+            x = x.to(torch.bfloat16 if w.dtype == "bf16" else torch.float32).contiguous()
+            h = None
+            if w.history is not None:
+                rng = np.random.default_rng(5000 + s)
+                hh = synth.zipf_ids(rng, 1.1, w.history.shape, w.V, rng.permutation(w.V))
+                h = torch.from_numpy(hh).to(dev)
+        sets.append((x, h))
+    return sets
+
+
+def cpu_baseline(w, seconds: float):
+    from oracle import oracle as o
+    from whallm_amd import synth
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = max(1, min(cores, 16))
+    p = synth.oracle_params(w, o.make_params)
+    o.sample_faithful(w.logits_f32[:1], p[:1], w.uniforms[:1], None if w.history is None else w.history[:1],
+                      None if w.history_len is None else w.history_len[:1], threads=1)
+    rows = 0
+    t0 = time.perf_counter()
+    while True:
+        o.sample_faithful(w.logits_f32, p, w.uniforms, w.history, w.history_len, threads=threads)
+        rows += w.B
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": rows / el, "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} rows ({rows // w.B} passes over the {w.B}-row seeded batch) of the same workload, "
+                      f"float32 replay of the reference op order (sort-based top-p/min-p, sequential cumsum), "
+                      f"OpenMP over rows, {el:.1f} s; host reports {cores} usable cores"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.steps)
+        return
+    import torch
+
+    from oracle import oracle as o
+    from whallm_amd import _lib, sampling, synth
+
+    dev = torch.device("cuda:0")
+    w = synth.SAMPLE_WORKLOADS[args.workload]()
+    prm = dict(w.params)
+    sets = make_sets(w, args.sets, dev)
+    hl = None if w.history_len is None else torch.from_numpy(w.history_len).to(dev)
+    kr = None if w.top_k_rows is None else torch.from_numpy(w.top_k_rows).to(dev)
+    u = torch.from_numpy(w.uniforms).to(dev)
+    tokens = torch.empty(w.B, dtype=torch.int32, device=dev)
+
+    # Parity on set 0 before timing.
+    tok0 = sampling.sample(sets[0][0], history=sets[0][1], history_len=hl, uniforms=u, top_k_rows=kr, **prm)
+    p = synth.oracle_params(w, o.make_params)
+    want, _ = o.sample(w.logits_f32, p, w.uniforms, w.history, w.history_len)
+    faithful, _ = o.sample_faithful(w.logits_f32, p, w.uniforms, w.history, w.history_len)
+    got = tok0.cpu().numpy()
+    parity = {"rows": int(w.B), "contract_bit_exact": bool(np.array_equal(got, want)),
+              "faithful_float32_agreement": float(np.mean(got == faithful))}
+
+    def step(i):
+        x, h = sets[i % len(sets)]
+        return sampling.sample(x, history=h, history_len=hl, uniforms=u, top_k_rows=kr, **prm)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)])
+    avg_s = float(kern_ms.mean()) / 1e3
+    nbytes = w.bytes_per_call()
+    achieved = nbytes / avg_s / 1e9
+    res = {
+        "metric": METRIC,
+        "value": w.B * args.steps / wall,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": w.name, "B": w.B, "V": w.V, "logits_dtype": w.dtype,
+                   "history": None if w.history is None else int(w.history.shape[1]),
+                   "input_sets": len(sets), "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "kernel_avg_us": avg_s * 1e6, "algorithmic_bytes": nbytes},
+        "parity": parity,
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()
