@@ -72,15 +72,16 @@ def test_exp_fix44_bit_exact(S, dev, oracle):
     assert np.array_equal(got, oracle.exp_fix44(d))
 
 
+@pytest.mark.parametrize("engine", ["auto", "exact"])
 @pytest.mark.parametrize("idx", [1, 2, 4, 5])
-def test_workload_parity_full_size(S, dev, oracle, idx):
+def test_workload_parity_full_size(S, dev, oracle, idx, engine):
     from whallm_amd import synth
 
     w = synth.SAMPLE_WORKLOADS[idx]()
     p = synth.oracle_params(w, oracle.make_params)
     ot, ok = oracle.sample(w.logits_f32, p, w.uniforms, w.history, w.history_len)
-    announce(f"wh_sample workload {idx}: {w.name}")
-    gt, gk = run_gpu_sample(S, w, dev)
+    announce(f"wh_sample workload {idx} engine={engine}: {w.name}")
+    gt, gk = run_gpu_sample(S, w, dev, engine=engine)
     assert np.array_equal(gk, ok), f"kept mismatch rows {np.nonzero(gk != ok)[0][:10]}"
     assert np.array_equal(gt, ot), f"token mismatch rows {np.nonzero(gt != ot)[0][:10]}"
     ft, _ = oracle.sample_faithful(w.logits_f32, p, w.uniforms, w.history, w.history_len)
@@ -101,7 +102,7 @@ def _random_case(rng, B, V):
     return x.astype(np.float32)
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(40))
 def test_random_parameters_parity(S, dev, oracle, seed):
     rng = np.random.default_rng(100 + seed)
     B = int(rng.integers(1, 40))
@@ -124,14 +125,17 @@ def test_random_parameters_parity(S, dev, oracle, seed):
     u[: max(1, B // 8)] = np.float32(0.0)
     p = oracle.make_params(B, temperature=T, top_p=top_p, top_k=top_k, min_p=min_p, chain=chain, **pen)
     ot, ok = oracle.sample(x, p, u, hist, hlen)
-    announce(f"wh_sample random seed={seed} B={B} V={V} chain={chain} T={T} p={top_p} k={top_k} minp={min_p} {pen}")
-    tok, kept = S.sample(torch.from_numpy(x).to(dev), temperature=T, top_p=top_p, top_k=top_k, min_p=min_p,
-                         chain=chain, history=torch.from_numpy(hist).to(dev), history_len=torch.from_numpy(hlen).to(dev),
-                         uniforms=torch.from_numpy(u).to(dev), return_kept=True, **pen)
-    tok, kept = tok.cpu().numpy(), kept.cpu().numpy()
-    if T > 0:
-        assert np.array_equal(kept, ok)
-    assert np.array_equal(tok, ot)
+    for engine in ("auto", "exact"):
+        announce(f"wh_sample random seed={seed} engine={engine} B={B} V={V} chain={chain} T={T} p={top_p} "
+                 f"k={top_k} minp={min_p} {pen}")
+        tok, kept = S.sample(torch.from_numpy(x).to(dev), temperature=T, top_p=top_p, top_k=top_k, min_p=min_p,
+                             chain=chain, history=torch.from_numpy(hist).to(dev),
+                             history_len=torch.from_numpy(hlen).to(dev), uniforms=torch.from_numpy(u).to(dev),
+                             return_kept=True, engine=engine, **pen)
+        tok, kept = tok.cpu().numpy(), kept.cpu().numpy()
+        if T > 0:
+            assert np.array_equal(kept, ok), engine
+        assert np.array_equal(tok, ot), engine
 
 
 @pytest.mark.parametrize("seed", range(4))

@@ -132,10 +132,12 @@ _workspaces: dict = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Cached device workspace (grown on demand, per device and stream)."""
+    """Cached device workspace per device and stream, zero-filled when it is
+    (re)allocated: the sampler's arrival counters must start at zero and every
+    completed call leaves them at zero."""
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf

@@ -1,0 +1,348 @@
+// wh_rowops.h -- per-row building blocks shared by the exact engine and the
+// sliced single-read engine: the penalised row view, filter predicates, radix
+// select over (value, id) composites, and the complete exact per-row
+// algorithm (exact_row), which the sliced engine also falls back to.
+#pragma once
+#include <cmath>
+
+#include "wh_common.h"
+#include "wh_internal.h"
+
+namespace wh {
+
+// ---------------------------------------------------------------------------
+// Row context: the row's logits plus its penalised history tokens.
+// ---------------------------------------------------------------------------
+struct RowCtx {
+  const float* xf;
+  const uint16_t* xb;
+  int V;
+  // penalty table (LDS), empty when hmask < 0
+  const int32_t* hkeys;
+  const float* hval;
+  const uint32_t* bitmap;
+  int hmask;
+  int hshift;
+
+  __device__ __forceinline__ float raw(int i) const { return xf ? xf[i] : bf16_to_f32(xb[i]); }
+
+  __device__ __forceinline__ float lookup(int i) const {
+    uint32_t s = ((uint32_t)i * 2654435761u) >> hshift;
+    while (hkeys[s] != i) s = (s + 1) & hmask;
+    return hval[s];
+  }
+  // Effective (penalised) value, with -0 mapped to +0.
+  __device__ __forceinline__ float val(int i) const {
+    if (hmask >= 0 && ((bitmap[i >> 5] >> (i & 31)) & 1u)) return lookup(i);
+    return raw(i) + 0.0f;
+  }
+};
+
+// Filter state: an element is kept iff every active predicate holds.
+struct Pred {
+  int none;      // nothing kept
+  int use_k;
+  uint64_t ck;   // keep iff comp_a >= ck
+  int use_p;
+  uint64_t cp;   // keep iff comp_p >= cp
+  int use_m;
+  float thr;     // keep iff value >= thr
+  float cov;     // keep iff value >= cov (restricts a search to a covered region)
+  __device__ __forceinline__ bool keep(int i, float l) const {
+    if (none) return false;
+    if (!(l >= cov)) return false;
+    uint32_t k = fkey(l);
+    if (use_k && comp_a(k, i) < ck) return false;
+    if (use_p && comp_p(k, i) < cp) return false;
+    if (use_m && !(l >= thr)) return false;
+    return true;
+  }
+};
+
+struct ExactSmem {
+  uint64_t hist[1024];
+  uint64_t scratch64[16];
+  float scratchf[16];
+  int scratchi[16];
+  uint64_t bcast64[4];
+  int bcasti[4];
+};
+
+// Penalty table setup in dynamic LDS.  Layout after ExactSmem:
+//   hkeys[hcap] int32, hpos[hcap] int32 (reused as float values), hcnt[hcap] int32,
+//   bitmap[(V+31)/32] uint32.
+// Only history tokens in [lo, hi) are entered; the bitmap covers [lo, hi).
+__device__ void build_penalties(const SampleKArgs& a, int b, RowCtx& rc, char* dyn, int lo, int hi) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int hcap = a.hcap;
+  int32_t* hkeys = (int32_t*)dyn;
+  int32_t* hpos = hkeys + hcap;
+  int32_t* hcnt = hpos + hcap;
+  uint32_t* bitmap = (uint32_t*)(hcnt + hcap);
+  const int words = (hi - lo + 31) >> 5;
+  rc.hkeys = hkeys;
+  rc.hval = (const float*)hpos;
+  rc.bitmap = bitmap;
+  rc.hmask = hcap - 1;
+  rc.hshift = 32 - a.hlog2;
+  for (int s = tid; s < hcap; s += nt) { hkeys[s] = -1; hpos[s] = -1; hcnt[s] = 0; }
+  for (int w = tid; w < words; w += nt) bitmap[w] = 0u;
+  __syncthreads();
+  int len = a.hist_len ? a.hist_len[b] : 0;
+  if (len < 0) len = 0;
+  if (len > a.hist_stride) len = (int)a.hist_stride;
+  const bool on_r = a.rep != 0.0f, on_p = a.pres != 0.0f, on_f = a.freq != 0.0f;
+  auto window = [len](int ctx) { return (ctx <= 0 || ctx > len) ? len : ctx; };
+  const int wr = on_r ? window(a.rep_ctx) : 0;
+  const int wp = on_p ? window(a.pres_ctx) : 0;
+  const int wf = on_f ? window(a.freq_ctx) : 0;
+  const int W = max(wr, max(wp, wf));
+  const int32_t* h = a.hist + (long long)b * a.hist_stride;
+  for (int j = len - W + tid; j < len; j += nt) {
+    int t = h[j];
+    if (t < lo || t >= hi || t >= a.V) continue;
+    uint32_t s = ((uint32_t)t * 2654435761u) >> rc.hshift;
+    while (true) {
+      int old = atomicCAS(&hkeys[s], -1, t);
+      if (old == -1 || old == t) break;
+      s = (s + 1) & rc.hmask;
+    }
+    atomicMax(&hpos[s], j);
+    if (j >= len - wf) atomicAdd(&hcnt[s], 1);
+    atomicOr(&bitmap[(t - lo) >> 5], 1u << ((t - lo) & 31));
+  }
+  __syncthreads();
+  for (int s = tid; s < hcap; s += nt) {
+    int t = hkeys[s];
+    if (t < 0) continue;
+    int lp = hpos[s];
+    int c = hcnt[s];
+    float v = rc.raw(t) + 0.0f;
+    if (on_r && lp >= len - wr) v = v < 0.0f ? v * a.rep : v / a.rep;
+    if (on_p && lp >= len - wp) v = v - a.pres;
+    if (on_f && c > 0) v = v - a.freq * (float)c;
+    ((float*)hpos)[s] = v + 0.0f;
+  }
+  __syncthreads();
+}
+
+// Element sources for radix_select: the whole penalised row, or a list of
+// (value, id) candidates held in LDS.
+struct RowSource {
+  const RowCtx* rc;
+  template <typename F>
+  __device__ __forceinline__ void each(F f) const {
+    for (int i = threadIdx.x; i < rc->V; i += blockDim.x) f(i, rc->val(i));
+  }
+};
+struct CandSource {
+  const float* v;
+  const int* id;
+  int n;
+  template <typename F>
+  __device__ __forceinline__ void each(F f) const {
+    for (int j = threadIdx.x; j < n; j += blockDim.x) f(id[j], v[j]);
+  }
+};
+
+enum { ORD_A = 0, ORD_P = 1, ORD_ID = 2 };
+
+template <int ORD>
+__device__ __forceinline__ uint64_t composite(float l, int i) {
+  if (ORD == ORD_ID) return (uint64_t)(0x3FFFF - i);  // vocabulary order
+  uint32_t k = fkey(l);
+  return ORD == ORD_P ? comp_p(k, i) : comp_a(k, i);
+}
+
+// Radix select in descending composite order (ORD_A: value desc, id asc;
+// ORD_P: value desc, id desc; ORD_ID: id asc).  Returns the composite of
+// the element at which the cumulative measure meas(i, l) over elements kept
+// by `pr` first reaches `target` (0 < target <= total).  10-bit digits: five
+// passes for the 50-bit value/id composites, two for ORD_ID.
+template <int ORD, typename Src, typename Meas>
+__device__ uint64_t radix_select(const Src& src, const Pred& pr, Meas meas, uint64_t target, ExactSmem& sm) {
+  const int tid = threadIdx.x;
+  constexpr int PASSES = ORD == ORD_ID ? 2 : 5;
+  uint64_t prefix = 0;
+  for (int pass = 0; pass < PASSES; ++pass) {
+    const int shift = 10 * (PASSES - 1 - pass);
+    for (int i = tid; i < 1024; i += blockDim.x) sm.hist[i] = 0;
+    __syncthreads();
+    src.each([&](int i, float l) {
+      if (!pr.keep(i, l)) return;
+      uint64_t c = composite<ORD>(l, i);
+      if ((c >> (shift + 10)) != prefix) return;
+      uint64_t w = meas(i, l);
+      if (w) atomicAdd((unsigned long long*)&sm.hist[(c >> shift) & 1023], (unsigned long long)w);
+    });
+    __syncthreads();
+    // suffix sums from the top bin: thread t owns bin 1023 - t
+    const int bin = 1023 - tid;
+    uint64_t hv = sm.hist[bin];
+    uint64_t tot;
+    uint64_t excl = block_exclusive_scan_u64(hv, sm.scratch64, &tot);
+    if (excl < target && excl + hv >= target) {
+      sm.bcast64[0] = (uint64_t)bin;
+      sm.bcast64[1] = excl;
+    }
+    __syncthreads();
+    prefix = (prefix << 10) | sm.bcast64[0];
+    target -= sm.bcast64[1];
+    __syncthreads();
+  }
+  return prefix;
+}
+
+__device__ __forceinline__ float chain_scale(int chain, float d, float invT, float Tc) {
+  return chain == WH_CHAIN_MLX ? d * invT : d / Tc;
+}
+
+// The whole exact algorithm for row b by one 1024-thread workgroup.
+__device__ void exact_row(const SampleKArgs& a, int b, char* dyn_smem, ExactSmem& sm) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int V = a.V;
+  RowCtx rc;
+  rc.V = V;
+  rc.xf = a.dtype == WH_DTYPE_F32 ? (const float*)a.logits + b * a.row_stride : nullptr;
+  rc.xb = a.dtype == WH_DTYPE_BF16 ? (const uint16_t*)a.logits + b * a.row_stride : nullptr;
+  rc.hmask = -1;
+  if (a.hcap > 0) build_penalties(a, b, rc, dyn_smem, 0, V);
+
+  const float T = a.T_rows ? a.T_rows[b] : a.T;
+  const float top_p = a.top_p_rows ? a.top_p_rows[b] : a.top_p;
+  const float min_p = a.min_p_rows ? a.min_p_rows[b] : a.min_p;
+  const int top_k = a.top_k_rows ? a.top_k_rows[b] : a.top_k;
+  float* out = a.out_rows ? a.out_rows + (long long)b * V : nullptr;
+
+  if (!(T > 0.0f)) {
+    // greedy: lowest index among the maxima (mx.argmax)
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int i = tid; i < V; i += nt) {
+      float l = rc.val(i);
+      if (bi == 0x7FFFFFFF || l > bv) { bv = l; bi = i; }
+      if (out) out[i] = l;
+    }
+    float m = block_reduce(bv, sm.scratchf, OpMaxF(), -INFINITY);
+    int cand = (bi != 0x7FFFFFFF && bv == m) ? bi : 0x7FFFFFFF;
+    int tok = block_reduce(cand, sm.scratchi, OpMinI(), 0x7FFFFFFF);
+    if (tid == 0) {
+      if (a.tokens) a.tokens[b] = tok == 0x7FFFFFFF ? 0 : tok;
+      if (a.kept) a.kept[b] = 1;
+    }
+    return;
+  }
+
+  float lmax = -INFINITY;
+  for (int i = tid; i < V; i += nt) lmax = fmaxf(lmax, rc.val(i));
+  const float m = block_reduce(lmax, sm.scratchf, OpMaxF(), -INFINITY);
+
+  const bool use_k = top_k > 0 && top_k < V;
+  const bool use_p = top_p > 0.0f && top_p < 1.0f;
+  const bool use_m = min_p != 0.0f;
+  const float theta = (float)(1.0 - (double)top_p);
+  Pred pr = {0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
+  auto mass = [m](int, float l) { return exp_fix44(l - m); };
+  auto one = [](int, float) { return (uint64_t)1; };
+
+  uint64_t Z = 0;
+  if (use_p) {
+    uint64_t z = 0;
+    if (m != -INFINITY)
+      for (int i = tid; i < V; i += nt) z += exp_fix44(rc.val(i) - m);
+    Z = block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
+  }
+  auto kept_mass = [&]() {
+    uint64_t s = 0;
+    if (m != -INFINITY)
+      for (int i = tid; i < V; i += nt) {
+        float l = rc.val(i);
+        if (pr.keep(i, l)) s += exp_fix44(l - m);
+      }
+    return block_reduce(s, sm.scratch64, OpSumU64(), (uint64_t)0);
+  };
+  auto kept_count = [&]() {
+    int c = 0;
+    for (int i = tid; i < V; i += nt) c += pr.keep(i, rc.val(i)) ? 1 : 0;
+    return block_reduce(c, sm.scratchi, OpSumI(), 0);
+  };
+  auto apply_p = [&](uint64_t S) {
+    uint64_t F = floor_theta_z(theta, Z);
+    if (S <= F) { pr.none = 1; return; }
+    uint64_t cp = radix_select<ORD_P>(RowSource{&rc}, pr, mass, S - F, sm);
+    pr.use_p = 1;
+    pr.cp = cp;
+  };
+  auto apply_m = [&]() {
+    const float c = a.min_p_rows ? (float)log((double)min_p) : a.min_p_log;
+    pr.use_m = 1;
+    pr.thr = m + c;
+  };
+
+  if (a.chain == WH_CHAIN_MLX) {
+    if (use_k) {
+      uint64_t ck = radix_select<ORD_A>(RowSource{&rc}, pr, one, (uint64_t)top_k, sm);
+      pr.use_k = 1;
+      pr.ck = ck;
+    }
+    if (use_p) apply_p(use_k ? kept_mass() : Z);
+    if (use_m && !pr.none) apply_m();
+  } else {
+    if (use_p) apply_p(Z);
+    if (use_m && !pr.none) apply_m();
+    if (use_k && !pr.none) {
+      int n_alive = kept_count();
+      if (n_alive > top_k) {
+        uint64_t ck = radix_select<ORD_A>(RowSource{&rc}, pr, one, (uint64_t)top_k, sm);
+        pr.use_k = 1;
+        pr.ck = ck;
+      }
+    }
+  }
+
+  // Draw: per-thread contiguous segments, integer inverse CDF in vocab order.
+  const float invT = (float)(1.0 / (double)T);
+  const float Tc = (float)fmax((double)T, 1e-5);
+  const int seg = (V + nt - 1) / nt;
+  const int lo = min(V, tid * seg), hi = min(V, lo + seg);
+  uint64_t s = 0;
+  int cnt = 0;
+  for (int i = lo; i < hi; ++i) {
+    float l = rc.val(i);
+    if (!pr.keep(i, l)) continue;
+    ++cnt;
+    s += exp_fix44(chain_scale(a.chain, l - m, invT, Tc));
+  }
+  uint64_t ZV;
+  uint64_t excl = block_exclusive_scan_u64(s, sm.scratch64, &ZV);
+  const int nkept = block_reduce(cnt, sm.scratchi, OpSumI(), 0);
+  if (a.tokens) {
+    const uint64_t tgt = ZV ? draw_target(a.u[b], ZV) : 0;
+    if (ZV == 0) {
+      if (tid == 0) a.tokens[b] = 0;
+    } else if (excl <= tgt && tgt < excl + s) {
+      uint64_t c = excl;
+      for (int i = lo; i < hi; ++i) {
+        float l = rc.val(i);
+        if (!pr.keep(i, l)) continue;
+        c += exp_fix44(chain_scale(a.chain, l - m, invT, Tc));
+        if (c > tgt) { a.tokens[b] = i; break; }
+      }
+    }
+  }
+  if (a.kept && tid == 0) a.kept[b] = nkept;
+  if (out && a.out_mode == WH_OUT_MASKED) {
+    for (int i = tid; i < V; i += nt) {
+      float l = rc.val(i);
+      out[i] = pr.keep(i, l) ? l : -INFINITY;
+    }
+  } else if (out) {
+    const double lz = log(ldexp((double)ZV, -44));
+    for (int i = tid; i < V; i += nt) {
+      float l = rc.val(i);
+      out[i] = pr.keep(i, l) ? (float)((double)chain_scale(a.chain, l - m, invT, Tc) - lz) : -INFINITY;
+    }
+  }
+}
+
+}  // namespace wh

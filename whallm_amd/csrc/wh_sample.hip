@@ -15,315 +15,14 @@
 // probability mass for top-p -- and the draw is an inverse CDF over integer
 // weights in vocabulary order, so results are bit-identical to the CPU
 // oracle whatever the reduction order.
-#include "wh_common.h"
-#include "wh_internal.h"
-
-#include <cmath>
+#include "wh_rowops.h"
 
 namespace wh {
-
-// ---------------------------------------------------------------------------
-// Row context: the row's logits plus its penalised history tokens.
-// ---------------------------------------------------------------------------
-struct RowCtx {
-  const float* xf;
-  const uint16_t* xb;
-  int V;
-  // penalty table (LDS), empty when hmask < 0
-  const int32_t* hkeys;
-  const float* hval;
-  const uint32_t* bitmap;
-  int hmask;
-  int hshift;
-
-  __device__ __forceinline__ float raw(int i) const { return xf ? xf[i] : bf16_to_f32(xb[i]); }
-
-  __device__ __forceinline__ float lookup(int i) const {
-    uint32_t s = ((uint32_t)i * 2654435761u) >> hshift;
-    while (hkeys[s] != i) s = (s + 1) & hmask;
-    return hval[s];
-  }
-  // Effective (penalised) value, with -0 mapped to +0.
-  __device__ __forceinline__ float val(int i) const {
-    if (hmask >= 0 && ((bitmap[i >> 5] >> (i & 31)) & 1u)) return lookup(i);
-    return raw(i) + 0.0f;
-  }
-};
-
-// Filter state: an element is kept iff every active predicate holds.
-struct Pred {
-  int none;      // nothing kept
-  int use_k;
-  uint64_t ck;   // keep iff comp_a >= ck
-  int use_p;
-  uint64_t cp;   // keep iff comp_p >= cp
-  int use_m;
-  float thr;     // keep iff value >= thr
-  __device__ __forceinline__ bool keep(int i, float l) const {
-    if (none) return false;
-    uint32_t k = fkey(l);
-    if (use_k && comp_a(k, i) < ck) return false;
-    if (use_p && comp_p(k, i) < cp) return false;
-    if (use_m && !(l >= thr)) return false;
-    return true;
-  }
-};
-
-struct ExactSmem {
-  uint64_t hist[1024];
-  uint64_t scratch64[16];
-  float scratchf[16];
-  int scratchi[16];
-  uint64_t bcast64[4];
-  int bcasti[4];
-};
-
-// Penalty table setup in dynamic LDS.  Layout after ExactSmem:
-//   hkeys[hcap] int32, hpos[hcap] int32 (reused as float values), hcnt[hcap] int32,
-//   bitmap[(V+31)/32] uint32.
-__device__ void build_penalties(const SampleKArgs& a, int b, RowCtx& rc, char* dyn) {
-  const int tid = threadIdx.x, nt = blockDim.x;
-  const int hcap = a.hcap;
-  int32_t* hkeys = (int32_t*)dyn;
-  int32_t* hpos = hkeys + hcap;
-  int32_t* hcnt = hpos + hcap;
-  uint32_t* bitmap = (uint32_t*)(hcnt + hcap);
-  const int words = (a.V + 31) >> 5;
-  rc.hkeys = hkeys;
-  rc.hval = (const float*)hpos;
-  rc.bitmap = bitmap;
-  rc.hmask = hcap - 1;
-  rc.hshift = 32 - a.hlog2;
-  for (int s = tid; s < hcap; s += nt) { hkeys[s] = -1; hpos[s] = -1; hcnt[s] = 0; }
-  for (int w = tid; w < words; w += nt) bitmap[w] = 0u;
-  __syncthreads();
-  int len = a.hist_len ? a.hist_len[b] : 0;
-  if (len < 0) len = 0;
-  if (len > a.hist_stride) len = (int)a.hist_stride;
-  const bool on_r = a.rep != 0.0f, on_p = a.pres != 0.0f, on_f = a.freq != 0.0f;
-  auto window = [len](int ctx) { return (ctx <= 0 || ctx > len) ? len : ctx; };
-  const int wr = on_r ? window(a.rep_ctx) : 0;
-  const int wp = on_p ? window(a.pres_ctx) : 0;
-  const int wf = on_f ? window(a.freq_ctx) : 0;
-  const int W = max(wr, max(wp, wf));
-  const int32_t* h = a.hist + (long long)b * a.hist_stride;
-  for (int j = len - W + tid; j < len; j += nt) {
-    int t = h[j];
-    if (t < 0 || t >= a.V) continue;
-    uint32_t s = ((uint32_t)t * 2654435761u) >> rc.hshift;
-    while (true) {
-      int old = atomicCAS(&hkeys[s], -1, t);
-      if (old == -1 || old == t) break;
-      s = (s + 1) & rc.hmask;
-    }
-    atomicMax(&hpos[s], j);
-    if (j >= len - wf) atomicAdd(&hcnt[s], 1);
-    atomicOr(&bitmap[t >> 5], 1u << (t & 31));
-  }
-  __syncthreads();
-  for (int s = tid; s < hcap; s += nt) {
-    int t = hkeys[s];
-    if (t < 0) continue;
-    int lp = hpos[s];
-    int c = hcnt[s];
-    float v = rc.raw(t) + 0.0f;
-    if (on_r && lp >= len - wr) v = v < 0.0f ? v * a.rep : v / a.rep;
-    if (on_p && lp >= len - wp) v = v - a.pres;
-    if (on_f && c > 0) v = v - a.freq * (float)c;
-    ((float*)hpos)[s] = v + 0.0f;
-  }
-  __syncthreads();
-}
-
-// Radix select over 50-bit composites in descending order: returns the
-// composite of the element at which the cumulative measure (count, or the
-// fixed-point mass exp_fix44(l - m)) of kept elements first reaches
-// `target` (> 0, <= total).  Five passes of 10-bit digits.
-template <bool MASS, bool ORDER_P>
-__device__ uint64_t radix_select(const RowCtx& rc, const Pred& pr, float m, uint64_t target, ExactSmem& sm) {
-  const int tid = threadIdx.x, nt = blockDim.x;
-  uint64_t prefix = 0;
-  for (int pass = 0; pass < 5; ++pass) {
-    const int shift = 40 - 10 * pass;
-    for (int i = tid; i < 1024; i += nt) sm.hist[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < rc.V; i += nt) {
-      float l = rc.val(i);
-      if (!pr.keep(i, l)) continue;
-      uint32_t k = fkey(l);
-      uint64_t c = ORDER_P ? comp_p(k, i) : comp_a(k, i);
-      if ((c >> (shift + 10)) != prefix) continue;
-      uint64_t meas = MASS ? exp_fix44(l - m) : 1ull;
-      if (meas) atomicAdd((unsigned long long*)&sm.hist[(c >> shift) & 1023], (unsigned long long)meas);
-    }
-    __syncthreads();
-    // suffix sums from the top bin: thread t owns bin 1023 - t
-    const int bin = 1023 - tid;
-    uint64_t hv = (tid < 1024) ? sm.hist[bin] : 0;
-    uint64_t tot;
-    uint64_t excl = block_exclusive_scan_u64(hv, sm.scratch64, &tot);
-    if (tid < 1024 && excl < target && excl + hv >= target) {
-      sm.bcast64[0] = (uint64_t)bin;
-      sm.bcast64[1] = excl;
-    }
-    __syncthreads();
-    prefix = (prefix << 10) | sm.bcast64[0];
-    target -= sm.bcast64[1];
-    __syncthreads();
-  }
-  return prefix;
-}
-
-__device__ __forceinline__ float chain_scale(int chain, float d, float invT, float Tc) {
-  return chain == WH_CHAIN_MLX ? d * invT : d / Tc;
-}
 
 __global__ void __launch_bounds__(1024) sample_exact_kernel(SampleKArgs a) {
   extern __shared__ __align__(16) char dyn_smem[];
   __shared__ ExactSmem sm;
-  const int b = blockIdx.x;
-  const int tid = threadIdx.x, nt = blockDim.x;
-  const int V = a.V;
-  RowCtx rc;
-  rc.V = V;
-  rc.xf = a.dtype == WH_DTYPE_F32 ? (const float*)a.logits + b * a.row_stride : nullptr;
-  rc.xb = a.dtype == WH_DTYPE_BF16 ? (const uint16_t*)a.logits + b * a.row_stride : nullptr;
-  rc.hmask = -1;
-  if (a.hcap > 0) build_penalties(a, b, rc, dyn_smem);
-
-  const float T = a.T_rows ? a.T_rows[b] : a.T;
-  const float top_p = a.top_p_rows ? a.top_p_rows[b] : a.top_p;
-  const float min_p = a.min_p_rows ? a.min_p_rows[b] : a.min_p;
-  const int top_k = a.top_k_rows ? a.top_k_rows[b] : a.top_k;
-  float* out = a.out_rows ? a.out_rows + (long long)b * V : nullptr;
-
-  if (!(T > 0.0f)) {
-    // greedy: lowest index among the maxima (mx.argmax)
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    for (int i = tid; i < V; i += nt) {
-      float l = rc.val(i);
-      if (bi == 0x7FFFFFFF || l > bv) { bv = l; bi = i; }
-      if (out) out[i] = l;
-    }
-    float m = block_reduce(bv, sm.scratchf, OpMaxF(), -INFINITY);
-    int cand = (bi != 0x7FFFFFFF && bv == m) ? bi : 0x7FFFFFFF;
-    int tok = block_reduce(cand, sm.scratchi, OpMinI(), 0x7FFFFFFF);
-    if (tid == 0) {
-      if (a.tokens) a.tokens[b] = tok == 0x7FFFFFFF ? 0 : tok;
-      if (a.kept) a.kept[b] = 1;
-    }
-    return;
-  }
-
-  float lmax = -INFINITY;
-  for (int i = tid; i < V; i += nt) lmax = fmaxf(lmax, rc.val(i));
-  const float m = block_reduce(lmax, sm.scratchf, OpMaxF(), -INFINITY);
-
-  const bool use_k = top_k > 0 && top_k < V;
-  const bool use_p = top_p > 0.0f && top_p < 1.0f;
-  const bool use_m = min_p != 0.0f;
-  const float theta = (float)(1.0 - (double)top_p);
-  Pred pr = {0, 0, 0, 0, 0, 0, 0.0f};
-
-  uint64_t Z = 0;
-  if (use_p) {
-    uint64_t z = 0;
-    if (m != -INFINITY)
-      for (int i = tid; i < V; i += nt) z += exp_fix44(rc.val(i) - m);
-    Z = block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
-  }
-  auto kept_mass = [&]() {
-    uint64_t s = 0;
-    if (m != -INFINITY)
-      for (int i = tid; i < V; i += nt) {
-        float l = rc.val(i);
-        if (pr.keep(i, l)) s += exp_fix44(l - m);
-      }
-    return block_reduce(s, sm.scratch64, OpSumU64(), (uint64_t)0);
-  };
-  auto kept_count = [&]() {
-    int c = 0;
-    for (int i = tid; i < V; i += nt) c += pr.keep(i, rc.val(i)) ? 1 : 0;
-    return block_reduce(c, sm.scratchi, OpSumI(), 0);
-  };
-  auto apply_p = [&](uint64_t S) {
-    uint64_t F = floor_theta_z(theta, Z);
-    if (S <= F) { pr.none = 1; return; }
-    uint64_t cp = radix_select<true, true>(rc, pr, m, S - F, sm);
-    pr.use_p = 1;
-    pr.cp = cp;
-  };
-  auto apply_m = [&]() {
-    const float c = a.min_p_rows ? (float)log((double)min_p) : a.min_p_log;
-    pr.use_m = 1;
-    pr.thr = m + c;
-  };
-
-  if (a.chain == WH_CHAIN_MLX) {
-    if (use_k) {
-      uint64_t ck = radix_select<false, false>(rc, pr, m, (uint64_t)top_k, sm);
-      pr.use_k = 1;
-      pr.ck = ck;
-    }
-    if (use_p) apply_p(use_k ? kept_mass() : Z);
-    if (use_m && !pr.none) apply_m();
-  } else {
-    if (use_p) apply_p(Z);
-    if (use_m && !pr.none) apply_m();
-    if (use_k && !pr.none) {
-      int n_alive = kept_count();
-      if (n_alive > top_k) {
-        uint64_t ck = radix_select<false, false>(rc, pr, m, (uint64_t)top_k, sm);
-        pr.use_k = 1;
-        pr.ck = ck;
-      }
-    }
-  }
-
-  // Draw: per-thread contiguous segments, integer inverse CDF in vocab order.
-  const float invT = (float)(1.0 / (double)T);
-  const float Tc = (float)fmax((double)T, 1e-5);
-  const int seg = (V + nt - 1) / nt;
-  const int lo = min(V, tid * seg), hi = min(V, lo + seg);
-  uint64_t s = 0;
-  int cnt = 0;
-  for (int i = lo; i < hi; ++i) {
-    float l = rc.val(i);
-    if (!pr.keep(i, l)) continue;
-    ++cnt;
-    s += exp_fix44(chain_scale(a.chain, l - m, invT, Tc));
-  }
-  uint64_t ZV;
-  uint64_t excl = block_exclusive_scan_u64(s, sm.scratch64, &ZV);
-  const int nkept = block_reduce(cnt, sm.scratchi, OpSumI(), 0);
-  if (a.tokens) {
-    const uint64_t tgt = ZV ? draw_target(a.u[b], ZV) : 0;
-    if (ZV == 0) {
-      if (tid == 0) a.tokens[b] = 0;
-    } else if (excl <= tgt && tgt < excl + s) {
-      uint64_t c = excl;
-      for (int i = lo; i < hi; ++i) {
-        float l = rc.val(i);
-        if (!pr.keep(i, l)) continue;
-        c += exp_fix44(chain_scale(a.chain, l - m, invT, Tc));
-        if (c > tgt) { a.tokens[b] = i; break; }
-      }
-    }
-  }
-  if (a.kept && tid == 0) a.kept[b] = nkept;
-  if (out && a.out_mode == WH_OUT_MASKED) {
-    for (int i = tid; i < V; i += nt) {
-      float l = rc.val(i);
-      out[i] = pr.keep(i, l) ? l : -INFINITY;
-    }
-  } else if (out) {
-    const double lz = log(ldexp((double)ZV, -44));
-    for (int i = tid; i < V; i += nt) {
-      float l = rc.val(i);
-      out[i] = pr.keep(i, l) ? (float)((double)chain_scale(a.chain, l - m, invT, Tc) - lz) : -INFINITY;
-    }
-  }
+  exact_row(a, blockIdx.x, dyn_smem, sm);
 }
 
 // In-place penalty processors (the unfused drop-in for make_logits_processors).
@@ -334,7 +33,7 @@ __global__ void __launch_bounds__(1024) penalties_kernel(SampleKArgs a) {
   rc.V = a.V;
   rc.xf = a.dtype == WH_DTYPE_F32 ? (const float*)a.logits + b * a.row_stride : nullptr;
   rc.xb = a.dtype == WH_DTYPE_BF16 ? (const uint16_t*)a.logits + b * a.row_stride : nullptr;
-  build_penalties(a, b, rc, dyn_smem);
+  build_penalties(a, b, rc, dyn_smem, 0, a.V);
   for (int s = threadIdx.x; s < a.hcap; s += blockDim.x) {
     int t = rc.hkeys[s];
     if (t < 0) continue;

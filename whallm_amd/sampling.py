@@ -108,7 +108,7 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
            repetition_context: int = 20, presence_context: int = 20, frequency_context: int = 20,
            uniforms: torch.Tensor | None = None, generator: torch.Generator | None = None,
            temperature_rows=None, top_p_rows=None, min_p_rows=None, top_k_rows=None,
-           return_logprobs: bool = False, return_kept: bool = False):
+           return_logprobs: bool = False, return_kept: bool = False, engine: str = "auto"):
     """Fused decode-step token selection for B rows (one kernel launch).
 
     chain "mlx": mlx_lm make_sampler order (top_k -> top_p -> min_p, then
@@ -121,6 +121,8 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
 
     Returns int32 tokens [B]; with return_logprobs (chain "whallm" only) also
     the sampling_logprobs rows [B, V]; with return_kept the kept-set sizes.
+    engine "exact" forces the multi-pass engine (no workspace) -- both
+    engines return identical results; "auto" picks the sliced single-read one.
     """
     logits, dt = _as_rows(logits)
     L.require_device(logits)
@@ -144,10 +146,11 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
     a.kept_count = L.ptr(kept)
     a.logprobs_out = L.ptr(out)
     a.out_mode = L.OUT_LOGPROBS
-    nb = L.lib().wh_sample_workspace_bytes(B, V)
-    ws = L.workspace(dev, nb)
-    a.workspace = ws.data_ptr()
-    a.workspace_bytes = ws.numel()
+    if engine != "exact":
+        nb = L.lib().wh_sample_workspace_bytes(B, V)
+        ws = L.workspace(dev, nb)
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws.numel()
     L.check(L.lib().wh_sample(ctypes.byref(a), ctypes.c_void_p(L.stream_of(logits))))
     del keep
     res = [tokens]
@@ -162,7 +165,7 @@ def filter_rows(logits: torch.Tensor, *, chain="whallm", temperature: float = 1.
                 top_k: int = 0, min_p: float = 0.0, out_mode: int = L.OUT_LOGPROBS,
                 history=None, history_len=None, repetition_penalty: float = 0.0, presence_penalty: float = 0.0,
                 frequency_penalty: float = 0.0, repetition_context: int = 20, presence_context: int = 20,
-                frequency_context: int = 20) -> torch.Tensor:
+                frequency_context: int = 20, engine: str = "auto") -> torch.Tensor:
     """Filtered rows without a draw: OUT_LOGPROBS gives Whallm's
     sampling_logprobs row, OUT_MASKED the input row with filtered entries -inf."""
     logits, dt = _as_rows(logits)
@@ -175,9 +178,10 @@ def filter_rows(logits: torch.Tensor, *, chain="whallm", temperature: float = 1.
                       presence_context, frequency_context, (None, None, None, None))
     a.logprobs_out = out.data_ptr()
     a.out_mode = out_mode
-    ws = L.workspace(logits.device, L.lib().wh_sample_workspace_bytes(B, V))
-    a.workspace = ws.data_ptr()
-    a.workspace_bytes = ws.numel()
+    if engine != "exact":
+        ws = L.workspace(logits.device, L.lib().wh_sample_workspace_bytes(B, V))
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws.numel()
     L.check(L.lib().wh_sample(ctypes.byref(a), ctypes.c_void_p(L.stream_of(logits))))
     del keep
     return out
