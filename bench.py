@@ -149,8 +149,10 @@ def main():
     want, _ = o.sample(w.logits_f32, p, w.uniforms, w.history, w.history_len)
     faithful, _ = o.sample_faithful(w.logits_f32, p, w.uniforms, w.history, w.history_len)
     got = tok0.cpu().numpy()
+    paths = sampling.last_paths(dev, w.B).cpu().numpy()
     parity = {"rows": int(w.B), "contract_bit_exact": bool(np.array_equal(got, want)),
-              "faithful_float32_agreement": float(np.mean(got == faithful))}
+              "faithful_float32_agreement": float(np.mean(got == faithful)),
+              "rows_exact_fallback": int(np.sum(paths == 1))}
 
     def step(i):
         x, h = sets[i % len(sets)]

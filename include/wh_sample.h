@@ -101,10 +101,9 @@ typedef struct wh_sample_args {
                                 entries set to -inf, no temperature (mlx_lm apply_top_k /
                                 apply_top_p / apply_min_p) */
   int32_t reserved;
-  void* workspace;           /* device, wh_sample_workspace_bytes(B, V) bytes, zero-filled
-                                before its first use; every completed call leaves it ready
-                                for the next.  One workspace per stream: calls that overlap
-                                on one workspace race.  NULL selects the slower
+  void* workspace;           /* device, wh_sample_workspace_bytes(B, V) bytes, contents need
+                                no initialisation.  One workspace per stream: calls that
+                                overlap on one workspace race.  NULL selects the slower
                                 multi-pass engine, which needs none. */
   size_t workspace_bytes;
 } wh_sample_args;

@@ -132,9 +132,7 @@ _workspaces: dict = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Cached device workspace per device and stream, zero-filled when it is
-    (re)allocated: the sampler's arrival counters must start at zero and every
-    completed call leaves them at zero."""
+    """Cached device workspace per device and stream (grown on demand)."""
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:

@@ -1,43 +1,54 @@
 // wh_fast.hip -- the sliced single-read sampler engine for gfx950.
 //
-// A row of V logits is cut into G slices; each slice is owned by one
-// 1024-thread workgroup that reads it from HBM exactly once (16-byte loads,
-// all issued up front, held in VGPRs).  All G workgroups of a row are placed
-// on the same XCD (workgroup ids are dealt to the 8 XCDs round robin), so the
-// merge reads each other's results through one L2.
+// Two kernels per call.
 //
-// Per slice: penalties for the slice's history tokens (LDS hash), the local
-// max, a float estimate of sum exp(l - m_s) for top-p certification, and the
-// candidates -- every slice element at or above a local threshold that is
-// provably below the row's kept set:
-//   rule M (min-p active):      tau_s = fl(m_s + ln min_p)  <= the row's min-p cut
-//   rule K (top-k bounds the kept set): tau_s = the slice's k-th largest value
-//   rule P (top-p only):        tau_s = the slice's (cap/2)-th largest value
-// The last workgroup of the row to arrive merges the slices' candidates and
-// decides with the exact integer contract (fixed-point masses exp_fix44);
-// the normaliser Z, which needs every element, is known only to within a
-// proven relative bound from the float estimates, so a top-p cut is taken
-// only if it is the same at both ends of the bound.  Whenever the
-// candidates cannot settle the row (capacity overflow, an ambiguous cut, no
-// filter at all) the merging workgroup runs the exact engine on the row.
+// slice_kernel: a row of V logits is cut into G slices; each slice is owned
+// by one 1024-thread workgroup that reads it from HBM exactly once (16-byte
+// loads, all issued up front, held in VGPRs) and reduces it to a summary:
+//   * the penalties for the slice's history tokens (LDS hash, values taken
+//     from the registers that hold the logits -- no second read),
+//   * the slice max m_s (and, for greedy rows, the lowest index attaining it),
+//   * the candidates: every slice element at or above a threshold tau_s that
+//     is provably below the row's kept set --
+//       rule M (min-p active):   tau_s = fl(m_s + ln min_p)  <= the row's cut
+//       rule K (top-k bounds the kept set): tau_s = the slice's k-th largest
+//       rule P (top-p only):     tau_s = the slice's cap/2-th largest,
+//   * bounds on the normaliser Z = sum_i exp_fix44(l_i - m): the exact
+//     fixed-point mass of the elements within 8 nats of m_s (a lower bound,
+//     with the count of the rest for an upper bound), plus a hardware-exp
+//     float estimate when top-p may cut without min-p behind it.
+// Workgroups never wait for each other: no fences, no atomics across them.
+//
+// merge_kernel: one workgroup per row.  Wave 0 merges the G summaries with
+// wave-level primitives (no block barriers): global max, exact fixed-point
+// masses of the candidates, top-k / top-p / min-p in the chain's order, and
+// the inverse-CDF draw over integer weights in vocabulary order -- the same
+// integer contract as the exact engine.  A top-p cut is taken only when it is
+// the same at both ends of the proven [Zlo, Zhi] interval.  A row the
+// candidates cannot settle (capacity overflow, an ambiguous cut, no filter at
+// all) is finished by the whole workgroup with the exact engine.
 #include "wh_rowops.h"
 
 namespace wh {
 
-constexpr int FT = 1024;          // threads per workgroup
-constexpr int FAST_RMAX = 8;      // max 16-byte loads per thread per slice
+constexpr int FT = 1024;          // slice-kernel threads per workgroup
+constexpr int FAST_RMAX = 16;     // max 16-byte loads per thread per slice
+constexpr float ZBAND = 8.0f;     // exact-mass band below the slice max, nats
 
 enum { RULE_GREEDY = 0, RULE_M = 1, RULE_K = 2, RULE_P = 3, RULE_ALL = 4 };
 
 struct SliceHdr {
-  float m;       // slice max (penalised)
-  float tau;     // every slice element >= tau is a candidate
-  int n;         // candidates written
-  int flags;     // 1: overflow -- the slice could not bound the kept set
-  double zf;     // sum over the slice of exp(l - m) (hardware exp)
-  float best_v;  // greedy: slice maximum
-  int best_i;    // greedy: lowest index attaining it
-  int pad[8];
+  float m;            // slice max (penalised)
+  float tau;          // every slice element >= tau is a candidate
+  int n;              // candidates written
+  int flags;          // 1: overflow / rule ALL -- the row needs the exact engine
+  unsigned long long zlo;  // sum of exp_fix44(l - m) over l >= zthr (exact)
+  float zthr;         // band floor for zlo
+  int ntier;          // elements in the band
+  int nrest;          // elements below the band
+  int best_i;         // greedy: lowest index attaining the max
+  double zf;          // sum of exp(l - m) over the slice (hardware exp), < 0 if not computed
+  int pad[4];
 };
 static_assert(sizeof(SliceHdr) == 64, "SliceHdr layout");
 
@@ -46,7 +57,7 @@ struct FastPlan {
   int SL;         // slice length (multiple of the elements per 16-byte load)
   int cap;        // candidate capacity per slice
   int rule_cap;   // largest k (or top-p window) a slice may bound
-  int* counters;  // [B] arrival counters (zero between calls)
+  int* path;      // [B] 0: merged from candidates, 1: exact engine, 2: greedy
   SliceHdr* hdr;  // [B * G]
   int2* cand;     // [B * G * cap] (value bits, id)
 };
@@ -58,6 +69,30 @@ __device__ __forceinline__ int choose_rule(int chain, float T, bool use_k, bool 
   if (use_k) return k <= rule_cap ? RULE_K : RULE_ALL;
   if (use_p) return RULE_P;
   return RULE_ALL;
+}
+
+struct RowParams {
+  float T, top_p, min_p;
+  int top_k;
+  bool use_k, use_p, use_m;
+  int rule;
+};
+
+__device__ __forceinline__ RowParams row_params(const SampleKArgs& a, int b, int rule_cap) {
+  RowParams r;
+  r.T = a.T_rows ? a.T_rows[b] : a.T;
+  r.top_p = a.top_p_rows ? a.top_p_rows[b] : a.top_p;
+  r.min_p = a.min_p_rows ? a.min_p_rows[b] : a.min_p;
+  r.top_k = a.top_k_rows ? a.top_k_rows[b] : a.top_k;
+  r.use_k = r.top_k > 0 && r.top_k < a.V;
+  r.use_p = r.top_p > 0.0f && r.top_p < 1.0f;
+  r.use_m = r.min_p != 0.0f;
+  r.rule = choose_rule(a.chain, r.T, r.use_k, r.use_p, r.use_m, r.top_k, rule_cap);
+  return r;
+}
+
+__device__ __forceinline__ float min_p_log(const SampleKArgs& a, float min_p) {
+  return a.min_p_rows ? (float)log((double)min_p) : a.min_p_log;
 }
 
 // Element e of a 16-byte group (DT 0: 4 x float32, DT 1: 8 x bfloat16), -0 -> +0.
@@ -73,6 +108,7 @@ __device__ __forceinline__ float grp_elem(const uint4& v, int e) {
   const uint32_t x = comp(v, e >> 1);
   return __uint_as_float((e & 1) ? (x & 0xFFFF0000u) : (x << 16)) + 0.0f;
 }
+// Write -inf into slot e of a 16-byte group.
 template <int DT>
 __device__ __forceinline__ void grp_kill(uint4& v, int e) {
   if (DT == 0) { set_comp(v, e, 0xFF800000u); return; }
@@ -80,38 +116,49 @@ __device__ __forceinline__ void grp_kill(uint4& v, int e) {
   set_comp(v, e >> 1, (e & 1) ? ((x & 0x0000FFFFu) | 0xFF800000u) : ((x & 0xFFFF0000u) | 0x0000FF80u));
 }
 
-// Byte offset of the slice-phase candidate buffer in dynamic LDS.
+// Dynamic LDS layout of the slice kernel:
+//   [hkeys hcap][hpos/hval hcap][hcnt hcap][bitmap (SL+31)/32] | candidate buffer (cap int2)
 __host__ __device__ __forceinline__ size_t cand_buf_offset(int hcap, int SL) {
   const size_t o = hcap > 0 ? (size_t)hcap * 12 + (size_t)((SL + 31) / 32) * 4 : 0;
   return (o + 15) / 16 * 16;
 }
 
+struct SliceSmem {
+  uint64_t hist64[1024];   // slice_kth counters (as 2048 x u32)
+  uint64_t s64[16];
+  double sd[16];
+  float sf[16];
+  int si[16];
+  uint64_t bc64[2];
+  int cnt;
+};
+
 // The slice's k-th largest value (k >= 1) over register elements and the
-// penalised list; -inf when the slice holds fewer than k elements.
+// penalised hash entries; -inf when the slice holds fewer than k elements.
 // 32-bit keys in three digit passes (11, 11, 10 bits), counts in LDS.
 template <int DT, int R>
-__device__ float slice_kth(const uint4 (&d)[R], int v0, int v1, const int* pl_id, const float* pl_v, int np,
-                           int k, ExactSmem& sm) {
+__device__ float slice_kth(const uint4 (&d)[R], int v0, int v1, const int* hk, const float* hv, int hcap,
+                           int k, SliceSmem& sm) {
   const int tid = threadIdx.x;
   constexpr int EPT = DT ? 8 : 4;
-  uint32_t* hist = (uint32_t*)sm.hist;  // 2048 counters
+  uint32_t* hist = (uint32_t*)sm.hist64;
   int cnt = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) cnt += (v0 + (r * FT + tid) * EPT < v1) ? EPT : 0;
-  for (int j = tid; j < np; j += FT) cnt++;
-  const int total = block_reduce(cnt, sm.scratchi, OpSumI(), 0);
+  for (int j = tid; j < hcap; j += FT) cnt += hk[j] >= 0 ? 1 : 0;
+  const int total = block_reduce(cnt, sm.si, OpSumI(), 0);
   if (total < k) return -INFINITY;
   uint32_t prefix = 0;
   uint32_t target = (uint32_t)k;
-  const int shifts[3] = {21, 10, 0};
-  const int bits[3] = {11, 11, 10};
+#pragma unroll
   for (int pass = 0; pass < 3; ++pass) {
-    const int sh = shifts[pass], nb = bits[pass];
+    const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const int nb = pass == 2 ? 10 : 11;
     const uint32_t mask = (1u << nb) - 1u;
     for (int i = tid; i < 2048; i += FT) hist[i] = 0;
     __syncthreads();
     auto add = [&](float l) {
-      uint32_t key = fkey(l);
+      const uint32_t key = fkey(l);
       if (pass > 0 && (key >> (sh + nb)) != prefix) return;
       atomicAdd(&hist[(key >> sh) & mask], 1u);
     };
@@ -123,407 +170,515 @@ __device__ float slice_kth(const uint4 (&d)[R], int v0, int v1, const int* pl_id
         for (int e = 0; e < EPT; ++e) add(grp_elem<DT>(d[r], e));
       }
     }
-    for (int j = tid; j < np; j += FT) add(pl_v[j]);
+    for (int j = tid; j < hcap; j += FT)
+      if (hk[j] >= 0) add(hv[j]);
     __syncthreads();
-    // descending scan: thread t owns bins 2047-2t (hi) and 2046-2t (lo) of the live range
     const int nbins = 1 << nb;
     const int hi = nbins - 1 - 2 * tid, lo = hi - 1;
     const uint64_t h_hi = hi >= 0 ? hist[hi] : 0, h_lo = lo >= 0 ? hist[lo] : 0;
     uint64_t tot;
-    const uint64_t excl = block_exclusive_scan_u64(h_hi + h_lo, sm.scratch64, &tot);
+    const uint64_t excl = block_exclusive_scan_u64(h_hi + h_lo, sm.s64, &tot);
     if (hi >= 0 && excl < target && excl + h_hi >= target) {
-      sm.bcast64[0] = (uint64_t)hi;
-      sm.bcast64[1] = excl;
+      sm.bc64[0] = (uint64_t)hi;
+      sm.bc64[1] = excl;
     } else if (lo >= 0 && excl + h_hi < target && excl + h_hi + h_lo >= target) {
-      sm.bcast64[0] = (uint64_t)lo;
-      sm.bcast64[1] = excl + h_hi;
+      sm.bc64[0] = (uint64_t)lo;
+      sm.bc64[1] = excl + h_hi;
     }
     __syncthreads();
-    prefix = (prefix << nb) | (uint32_t)sm.bcast64[0];
-    target -= (uint32_t)sm.bcast64[1];
+    prefix = (prefix << nb) | (uint32_t)sm.bc64[0];
+    target -= (uint32_t)sm.bc64[1];
     __syncthreads();
   }
   return key_to_float(prefix);
 }
 
-// Merge of one row by the last-arriving workgroup.
-__device__ void finalize_row(const SampleKArgs& a, const FastPlan& P, int b, int rule, float T, float top_p,
-                             float min_p, int top_k, bool use_k, bool use_p, bool use_m, char* dyn, ExactSmem& sm) {
-  const int tid = threadIdx.x;
-  const int G = P.G;
-  const SliceHdr* H = P.hdr + (long long)b * G;
-  __shared__ float s_m[16], s_tau[16], s_bv[16];
-  __shared__ int s_n[16], s_off[17], s_flag, s_bi[16];
-  __shared__ double s_zf[16];
-  if (tid < G) {
-    s_m[tid] = H[tid].m;
-    s_tau[tid] = H[tid].tau;
-    s_n[tid] = H[tid].n;
-    s_zf[tid] = H[tid].zf;
-    s_bv[tid] = H[tid].best_v;
-    s_bi[tid] = H[tid].best_i;
-  }
-  if (tid == 0) P.counters[b] = 0;  // all G slices have arrived: ready for the next call
-  __syncthreads();
-  if (tid == 0) {
-    int f = 0, off = 0;
-    for (int s = 0; s < G; ++s) {
-      f |= H[s].flags;
-      s_off[s] = off;
-      off += s_n[s];
-    }
-    s_off[G] = off;
-    s_flag = f;
-  }
-  __syncthreads();
-  float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
-
-  if (rule == RULE_GREEDY) {
-    if (tid == 0) {
-      float bv = s_bv[0];
-      int bi = s_bi[0];
-      for (int s = 1; s < G; ++s)
-        if (s_bv[s] > bv || (s_bv[s] == bv && s_bi[s] < bi)) { bv = s_bv[s]; bi = s_bi[s]; }
-      if (a.tokens) a.tokens[b] = bi;
-      if (a.kept) a.kept[b] = 1;
-    }
-    return;
-  }
-  if (rule == RULE_ALL || s_flag) {
-    exact_row(a, b, dyn, sm);
-    return;
-  }
-  float m = -INFINITY, tcov = -INFINITY;
-  for (int s = 0; s < G; ++s) { m = fmaxf(m, s_m[s]); tcov = fmaxf(tcov, s_tau[s]); }
-  const int N = s_off[G];
-  float* cv = (float*)dyn;
-  int* ci = (int*)(dyn + (size_t)G * P.cap * sizeof(float));
-  for (int s = 0; s < G; ++s) {
-    const int2* src = P.cand + ((long long)b * G + s) * P.cap;
-    for (int j = tid; j < s_n[s]; j += FT) {
-      int2 c = src[j];
-      cv[s_off[s] + j] = __int_as_float(c.x);
-      ci[s_off[s] + j] = c.y;
-    }
-  }
-  __syncthreads();
-  CandSource src{cv, ci, N};
-  Pred pr = {0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
-  auto mass = [m](int, float l) { return exp_fix44(l - m); };
-  auto one = [](int, float) { return (uint64_t)1; };
-  auto count = [&](const Pred& p) {
-    int c = 0;
-    src.each([&](int i, float l) { c += p.keep(i, l) ? 1 : 0; });
-    return block_reduce(c, sm.scratchi, OpSumI(), 0);
-  };
-  auto msum = [&](const Pred& p) {
-    uint64_t z = 0;
-    src.each([&](int i, float l) { if (p.keep(i, l)) z += exp_fix44(l - m); });
-    return block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
-  };
-  const float theta = (float)(1.0 - (double)top_p);
-  bool ambiguous = false;
-
-  // Top-p with the normaliser known to within [Zlo, Zhi] (fixed point, 44
-  // fractional bits).  S is the alive mass (exact when `s_exact`, else Z).
-  auto apply_p = [&](bool s_exact) {
-    double zt = 0.0;
-    for (int s = 0; s < G; ++s)
-      if (s_m[s] != -INFINITY) zt += s_zf[s] * exp((double)s_m[s] - (double)m);
-    // |Z/2^44 - zt| <= 1e-4 zt + 1e-6 (hardware-exp and float-sum error, with margin)
-    const double sc = 17592186044416.0;
-    const double zl = fmax(0.0, (zt * (1.0 - 1e-4) - 1e-6) * sc), zh = (zt * (1.0 + 1e-4) + 1e-6) * sc;
-    const uint64_t Zlo = (uint64_t)zl, Zhi = (uint64_t)ceil(zh);
-    long long Rlo, Rhi;
-    if (s_exact) {
-      const long long S = (long long)msum(pr);
-      Rlo = S - (long long)floor_theta_z(theta, Zhi);
-      Rhi = S - (long long)floor_theta_z(theta, Zlo);
-    } else {
-      Rlo = (long long)(Zlo - floor_theta_z(theta, Zlo));
-      Rhi = (long long)(Zhi - floor_theta_z(theta, Zhi));
-    }
-    if (Rhi <= 0) { pr.none = 1; return; }
-    if (Rlo <= 0) { ambiguous = true; return; }
-    Pred pc = pr;
-    pc.cov = tcov;
-    const long long Scov = (long long)msum(pc);
-    if (Rlo > Scov) {
-      // every covered element survives; the kept set stays inside the covered
-      // region only if a later filter confines it there (min-p cut >= every
-      // slice threshold, or the top-k set, all of which is covered)
-      if (rule == RULE_P) ambiguous = true;
-      return;
-    }
-    if (Rhi > Scov) { ambiguous = true; return; }
-    const uint64_t clo = radix_select<ORD_P>(src, pc, mass, (uint64_t)Rlo, sm);
-    const uint64_t chi = radix_select<ORD_P>(src, pc, mass, (uint64_t)Rhi, sm);
-    if (clo != chi) { ambiguous = true; return; }
-    pr.use_p = 1;
-    pr.cp = clo;
-  };
-  auto apply_m = [&]() {
-    const float c = a.min_p_rows ? (float)log((double)min_p) : a.min_p_log;
-    pr.use_m = 1;
-    pr.thr = m + c;
-  };
-  if (a.chain == WH_CHAIN_MLX && rule == RULE_K) {
-    // the candidates hold the whole top-k set (at least k of them)
-    if (use_k) {
-      pr.ck = radix_select<ORD_A>(src, pr, one, (uint64_t)top_k, sm);
-      pr.use_k = 1;
-    }
-    if (use_p) apply_p(use_k);
-    if (!ambiguous && use_m && !pr.none) apply_m();
-  } else if (a.chain == WH_CHAIN_MLX) {
-    // rule M or P: no top-p together with top-k here.  k -> min-p: the min-p
-    // set is a value prefix held by the candidates; if it has more than k
-    // members the row's first k (order A) are its first k, else top-k keeps
-    // all of it.
-    if (use_p) apply_p(false);
-    if (!ambiguous && use_m && !pr.none) apply_m();
-    if (!ambiguous && use_k && !pr.none && count(pr) > top_k) {
-      pr.ck = radix_select<ORD_A>(src, pr, one, (uint64_t)top_k, sm);
-      pr.use_k = 1;
-    }
-  } else {
-    if (use_p) apply_p(false);
-    if (!ambiguous && use_m && !pr.none) apply_m();
-    if (!ambiguous && use_k && !pr.none) {
-      if (count(pr) > top_k) {
-        pr.ck = radix_select<ORD_A>(src, pr, one, (uint64_t)top_k, sm);
-        pr.use_k = 1;
-      }
-    }
-  }
-  if (ambiguous) {
-    exact_row(a, b, dyn, sm);
-    return;
-  }
-  // Draw: integer inverse CDF in vocabulary order over the kept candidates.
-  const float invT = (float)(1.0 / (double)T);
-  const float Tc = (float)fmax((double)T, 1e-5);
-  auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, Tc)); };
-  uint64_t zv = 0;
-  int nk = 0;
-  src.each([&](int i, float l) {
-    if (pr.keep(i, l)) { zv += vw(i, l); ++nk; }
-  });
-  const uint64_t ZV = block_reduce(zv, sm.scratch64, OpSumU64(), (uint64_t)0);
-  const int nkept = block_reduce(nk, sm.scratchi, OpSumI(), 0);
-  if (a.tokens) {
-    int tok = 0;
-    if (ZV) {
-      const uint64_t tgt = draw_target(a.u[b], ZV);
-      tok = 0x3FFFF - (int)radix_select<ORD_ID>(src, pr, vw, tgt + 1, sm);
-    }
-    if (tid == 0) a.tokens[b] = tok;
-  }
-  if (tid == 0 && a.kept) a.kept[b] = nkept;
-  if (out) {
-    const double lz = log(ldexp((double)ZV, -44));
-    src.each([&](int i, float l) {
-      if (!pr.keep(i, l)) return;
-      out[i] = a.out_mode == WH_OUT_MASKED ? l : (float)((double)chain_scale(a.chain, l - m, invT, Tc) - lz);
-    });
-  }
-}
-
 template <int DT, int R>
-__global__ void __launch_bounds__(FT) sample_fast_kernel(SampleKArgs a, FastPlan P) {
+__global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   extern __shared__ __align__(16) char dyn[];
-  __shared__ ExactSmem sm;
-  __shared__ int s_cnt, s_np, s_last;
+  __shared__ SliceSmem sm;
   constexpr int EPT = DT ? 8 : 4;
   constexpr int ESZ = DT ? 2 : 4;
   const int tid = threadIdx.x;
-  const int bid = blockIdx.x, xcd = bid & 7, q = bid >> 3;
-  const int s = q % P.G, b = (q / P.G) * 8 + xcd;
-  if (b >= a.B) return;
+  const int b = blockIdx.x / P.G, s = blockIdx.x % P.G;
   const int V = a.V;
   const int v0 = s * P.SL, v1 = min(V, v0 + P.SL);
-
-  const float T = a.T_rows ? a.T_rows[b] : a.T;
-  const float top_p = a.top_p_rows ? a.top_p_rows[b] : a.top_p;
-  const float min_p = a.min_p_rows ? a.min_p_rows[b] : a.min_p;
-  const int top_k = a.top_k_rows ? a.top_k_rows[b] : a.top_k;
-  const bool use_k = top_k > 0 && top_k < V;
-  const bool use_p = top_p > 0.0f && top_p < 1.0f;
-  const bool use_m = min_p != 0.0f;
-  const int rule = choose_rule(a.chain, T, use_k, use_p, use_m, top_k, P.rule_cap);
-  float* out = a.out_rows ? a.out_rows + (long long)b * V : nullptr;
+  const RowParams rp = row_params(a, b, P.rule_cap);
   SliceHdr* hdr = P.hdr + (long long)b * P.G + s;
+  if (rp.rule == RULE_ALL) {
+    if (tid == 0) hdr->flags = 1;
+    return;
+  }
+  float* out = a.out_rows ? a.out_rows + (long long)b * V : nullptr;
 
-  if (rule != RULE_ALL) {
-    // 1. the slice, straight into registers
-    const char* rowp = (const char*)a.logits + (size_t)b * a.row_stride * ESZ;
-    uint4 d[R];
+  // 1. the slice, straight into registers
+  const char* rowp = (const char*)a.logits + (size_t)b * a.row_stride * ESZ;
+  uint4 d[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int g = v0 + (r * FT + tid) * EPT;
+    d[r] = make_uint4(0u, 0u, 0u, 0u);
+    if (g < v1) d[r] = *(const uint4*)(rowp + (size_t)g * ESZ);
+  }
+
+  // 2. penalties: history window -> LDS hash of the slice's tokens; the owner
+  //    of each penalised element computes its value from the register copy,
+  //    stores it in the hash and writes -inf into the register slot
+  const int hcap = a.hcap;
+  int32_t* hkeys = (int32_t*)dyn;
+  int32_t* hpos = hkeys + hcap;
+  int32_t* hcnt = hpos + hcap;
+  uint32_t* bm = (uint32_t*)(hcnt + hcap);
+  float* hval = (float*)hpos;
+  if (hcap > 0) {
+    const int words = (v1 - v0 + 31) >> 5;
+    for (int t = tid; t < hcap; t += FT) { hkeys[t] = -1; hpos[t] = -1; hcnt[t] = 0; }
+    for (int w = tid; w < words; w += FT) bm[w] = 0u;
+    int len = a.hist_len ? a.hist_len[b] : 0;
+    len = max(0, min(len, (int)a.hist_stride));
+    const bool on_r = a.rep != 0.0f, on_p = a.pres != 0.0f, on_f = a.freq != 0.0f;
+    auto window = [len](int ctx) { return (ctx <= 0 || ctx > len) ? len : ctx; };
+    const int wr = on_r ? window(a.rep_ctx) : 0;
+    const int wp = on_p ? window(a.pres_ctx) : 0;
+    const int wf = on_f ? window(a.freq_ctx) : 0;
+    const int W = max(wr, max(wp, wf));
+    const int32_t* h = a.hist + (long long)b * a.hist_stride;
+    __syncthreads();
+    const int hshift = 32 - a.hlog2, hmask = hcap - 1;
+    for (int j = len - W + tid; j < len; j += FT) {
+      const int t = h[j];
+      if (t < v0 || t >= v1) continue;
+      uint32_t q = ((uint32_t)t * 2654435761u) >> hshift;
+      while (true) {
+        const int old = atomicCAS(&hkeys[q], -1, t);
+        if (old == -1 || old == t) break;
+        q = (q + 1) & hmask;
+      }
+      atomicMax(&hpos[q], j);
+      if (j >= len - wf) atomicAdd(&hcnt[q], 1);
+      atomicOr(&bm[(t - v0) >> 5], 1u << ((t - v0) & 31));
+    }
+    __syncthreads();
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int g = v0 + (r * FT + tid) * EPT;
-      if (g < v1) d[r] = *(const uint4*)(rowp + (size_t)g * ESZ);
+      if (g < v1) {
+        const int o = g - v0;
+        const uint32_t bits = (bm[o >> 5] >> (o & 31)) & ((1u << EPT) - 1u);
+        if (bits) {
+#pragma unroll
+          for (int e = 0; e < EPT; ++e) {
+            if (!((bits >> e) & 1u)) continue;
+            const int t = g + e;
+            uint32_t q = ((uint32_t)t * 2654435761u) >> hshift;
+            while (hkeys[q] != t) q = (q + 1) & hmask;
+            const int lp = hpos[q], c = hcnt[q];
+            float v = grp_elem<DT>(d[r], e);
+            if (on_r && lp >= len - wr) v = v < 0.0f ? v * a.rep : v / a.rep;
+            if (on_p && lp >= len - wp) v = v - a.pres;
+            if (on_f && c > 0) v = v - a.freq * (float)c;
+            hval[q] = v + 0.0f;
+            grp_kill<DT>(d[r], e);
+          }
+        }
+      }
     }
-    // 2. penalties for the slice's history tokens; the penalised values go to
-    //    a list (ids pl_id, values pl_v) and their register copies become -inf
-    int np = 0;
-    const int* pl_id = nullptr;
-    const float* pl_v = nullptr;
-    if (a.hcap > 0) {
-      RowCtx rc;
-      rc.V = V;
-      rc.xf = DT == 0 ? (const float*)rowp : nullptr;
-      rc.xb = DT == 1 ? (const uint16_t*)rowp : nullptr;
-      build_penalties(a, b, rc, dyn, v0, v1);
-      int32_t* hkeys = (int32_t*)dyn;
-      float* hval = (float*)(hkeys + a.hcap);
-      int32_t* hcnt = hkeys + 2 * a.hcap;
-      const uint32_t* bm = (const uint32_t*)(hkeys + 3 * a.hcap);
-      // compact (key, value) pairs: read own slots, then write the list over
-      // hcnt (ids) and hkeys (values)
-      int kk[8];
-      float vv[8];
-      int nmine = 0;
-      for (int t = tid; t < a.hcap; t += FT) {
-        if (hkeys[t] >= 0) { kk[nmine] = hkeys[t]; vv[nmine] = hval[t]; ++nmine; }
+    __syncthreads();
+  }
+  auto each_pen = [&](auto f) {
+    for (int j = tid; j < hcap; j += FT) {
+      const int i = hkeys[j];
+      if (i >= 0) f(i, hval[j]);
+    }
+  };
+
+  // 3. slice max and, for greedy rows, the lowest index attaining it
+  float mx = -INFINITY;
+  int mi = 0x7FFFFFFF;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int g = v0 + (r * FT + tid) * EPT;
+    if (g < v1) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const float l = grp_elem<DT>(d[r], e);
+        if (mi == 0x7FFFFFFF || l > mx) { mx = l; mi = g + e; }
       }
-      if (tid == 0) s_np = 0;
-      __syncthreads();
-      for (int j = 0; j < nmine; ++j) {
-        int slot = atomicAdd(&s_np, 1);
-        hcnt[slot] = kk[j];
-        ((float*)hkeys)[slot] = vv[j];
-      }
+    }
+  }
+  each_pen([&](int i, float l) {
+    if (mi == 0x7FFFFFFF || l > mx || (l == mx && i < mi)) { mx = l; mi = i; }
+  });
+  const float ms = block_reduce(mx, sm.sf, OpMaxF(), -INFINITY);
+
+  if (rp.rule == RULE_GREEDY) {
+    const int cand = (mi != 0x7FFFFFFF && mx == ms) ? mi : 0x7FFFFFFF;
+    const int bi = block_reduce(cand, sm.si, OpMinI(), 0x7FFFFFFF);
+    if (out) {  // Whallm's sampling_logprobs returns the (penalised) logits at T == 0
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int g = v0 + (r * FT + tid) * EPT;
         if (g < v1) {
-          const int o = g - v0;
-          const uint32_t bits = (bm[o >> 5] >> (o & 31)) & ((1u << EPT) - 1u);
-          if (bits) {
 #pragma unroll
-            for (int e = 0; e < EPT; ++e)
-              if ((bits >> e) & 1u) grp_kill<DT>(d[r], e);
-          }
+          for (int e = 0; e < EPT; ++e) out[g + e] = grp_elem<DT>(d[r], e);
         }
       }
       __syncthreads();
-      np = s_np;
-      pl_id = hcnt;
-      pl_v = (const float*)hkeys;
+      each_pen([&](int i, float l) { out[i] = l; });
     }
-    // 3. slice max and, for greedy rows, the lowest index attaining it
-    float mx = -INFINITY;
-    int mi = 0x7FFFFFFF;
+    if (tid == 0) {
+      hdr->m = ms;
+      hdr->best_i = bi;
+      hdr->flags = 0;
+      hdr->n = 0;
+    }
+    return;
+  }
+
+  // 4. candidate threshold and the exact-mass band
+  float tau;
+  if (rp.rule == RULE_M) tau = ms + min_p_log(a, rp.min_p);
+  else tau = slice_kth<DT, R>(d, v0, v1, hkeys, hval, hcap, rp.rule == RULE_K ? rp.top_k : P.rule_cap, sm);
+  const float zthr = fminf(tau, ms - ZBAND);
+  const bool need_zf = rp.use_p && !rp.use_m;
+
+  // 5. one pass: candidates to LDS, band mass, optional float estimate
+  int2* buf = (int2*)(dyn + cand_buf_offset(hcap, P.SL));
+  if (tid == 0) sm.cnt = 0;
+  __syncthreads();
+  uint64_t zl = 0;
+  int ntier = 0, nall = 0;
+  float zs = 0.0f;
+  auto visit = [&](int i, float l) {
+    ++nall;
+    if (l >= zthr) {
+      if (l >= tau) {
+        const int slot = atomicAdd(&sm.cnt, 1);
+        if (slot < P.cap) buf[slot] = make_int2(__float_as_int(l), i);
+      }
+      ++ntier;
+      zl += exp_fix44(l - ms);
+    }
+    if (need_zf) zs += __expf(l - ms);
+  };
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int g = v0 + (r * FT + tid) * EPT;
+    if (g < v1) {
+      // penalised elements are visited once, through the hash, below
+      const uint32_t killed = hcap > 0 ? (bm[(g - v0) >> 5] >> ((g - v0) & 31)) & ((1u << EPT) - 1u) : 0u;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e)
+        if (!((killed >> e) & 1u)) visit(g + e, grp_elem<DT>(d[r], e));
+    }
+  }
+  each_pen([&](int i, float l) { visit(i, l); });
+  const uint64_t zlo = block_reduce(zl, sm.s64, OpSumU64(), (uint64_t)0);
+  const int ntier_b = block_reduce(ntier, sm.si, OpSumI(), 0);
+  const int nall_b = block_reduce(nall, sm.si, OpSumI(), 0);
+  const double zf = need_zf ? block_reduce((double)zs, sm.sd, OpSumF64(), 0.0) : -1.0;
+  __syncthreads();
+  const int n = sm.cnt;
+  const int nw = min(n, P.cap);
+  int2* gc = P.cand + ((long long)b * P.G + s) * P.cap;
+  for (int j = tid; j < nw; j += FT) gc[j] = buf[j];
+  if (out) {
+    // non-candidates are never kept; the merge overwrites the kept ones
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int g = v0 + (r * FT + tid) * EPT;
       if (g < v1) {
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) {
-          const float l = grp_elem<DT>(d[r], e);
-          if (mi == 0x7FFFFFFF || l > mx) { mx = l; mi = g + e; }
-        }
-      }
-    }
-    for (int j = tid; j < np; j += FT) {
-      const float l = pl_v[j];
-      const int i = pl_id[j];
-      if (mi == 0x7FFFFFFF || l > mx || (l == mx && i < mi)) { mx = l; mi = i; }
-    }
-    const float ms = block_reduce(mx, sm.scratchf, OpMaxF(), -INFINITY);
-
-    if (rule == RULE_GREEDY) {
-      const int cand = (mi != 0x7FFFFFFF && mx == ms) ? mi : 0x7FFFFFFF;
-      const int bi = block_reduce(cand, sm.scratchi, OpMinI(), 0x7FFFFFFF);
-      if (out) {  // Whallm's sampling_logprobs returns the (penalised) logits at T == 0
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const int g = v0 + (r * FT + tid) * EPT;
-          if (g < v1) {
-#pragma unroll
-            for (int e = 0; e < EPT; ++e) out[g + e] = grp_elem<DT>(d[r], e);
-          }
-        }
-        __syncthreads();
-        for (int j = tid; j < np; j += FT) out[pl_id[j]] = pl_v[j];
-      }
-      if (tid == 0) {
-        hdr->best_v = ms;
-        hdr->best_i = bi;
-        hdr->flags = 0;
-        hdr->n = 0;
-      }
-    } else {
-      // 4. candidate threshold
-      float tau;
-      if (rule == RULE_M) {
-        const float c = a.min_p_rows ? (float)log((double)min_p) : a.min_p_log;
-        tau = ms + c;
-      } else {
-        tau = slice_kth<DT, R>(d, v0, v1, pl_id, pl_v, np, rule == RULE_K ? top_k : P.rule_cap, sm);
-      }
-      // 5. compact the candidates into LDS, then to the workspace
-      int2* buf = (int2*)(dyn + cand_buf_offset(a.hcap, P.SL));
-      if (tid == 0) s_cnt = 0;
-      __syncthreads();
-      float zs = 0.0f;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int g = v0 + (r * FT + tid) * EPT;
-        if (g < v1) {
-#pragma unroll
-          for (int e = 0; e < EPT; ++e) {
-            const float l = grp_elem<DT>(d[r], e);
-            if (l >= tau) {
-              const int slot = atomicAdd(&s_cnt, 1);
-              if (slot < P.cap) buf[slot] = make_int2(__float_as_int(l), g + e);
-            }
-            if (use_p && ms != -INFINITY) zs += __expf(l - ms);
-          }
-        }
-      }
-      for (int j = tid; j < np; j += FT) {
-        const float l = pl_v[j];
-        if (l >= tau) {
-          const int slot = atomicAdd(&s_cnt, 1);
-          if (slot < P.cap) buf[slot] = make_int2(__float_as_int(l), pl_id[j]);
-        }
-        if (use_p && ms != -INFINITY) zs += __expf(l - ms);
-      }
-      const double zf = use_p ? block_reduce((double)zs, (double*)sm.scratch64, OpSumF64(), 0.0) : 0.0;
-      __syncthreads();
-      const int n = s_cnt;
-      const int nw = min(n, P.cap);
-      int2* gc = P.cand + ((long long)b * P.G + s) * P.cap;
-      for (int j = tid; j < nw; j += FT) gc[j] = buf[j];
-      if (out) {
-        // non-candidates are never kept; the merge overwrites the kept ones
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const int g = v0 + (r * FT + tid) * EPT;
-          if (g < v1) {
-#pragma unroll
-            for (int e = 0; e < EPT; ++e) out[g + e] = -INFINITY;
-          }
-        }
-      }
-      if (tid == 0) {
-        hdr->m = ms;
-        hdr->tau = tau;
-        hdr->n = nw;
-        hdr->flags = n > P.cap ? 1 : 0;
-        hdr->zf = zf;
+        for (int e = 0; e < EPT; ++e) out[g + e] = -INFINITY;
       }
     }
   }
-  // 6. arrival: the last slice of the row merges
-  __threadfence();
+  if (tid == 0) {
+    hdr->m = ms;
+    hdr->tau = tau;
+    hdr->n = nw;
+    hdr->flags = n > P.cap ? 1 : 0;
+    hdr->zlo = zlo;
+    hdr->zthr = zthr;
+    hdr->ntier = ntier_b;
+    hdr->nrest = nall_b - ntier_b;
+    hdr->zf = zf;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wave-level merge.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+struct MergeSmem {
+  uint64_t hist[1024];
+  uint64_t bc64[2];
+};
+
+struct WaveCands {
+  const float* v;
+  const int* id;
+  int n;
+  template <typename F>
+  __device__ __forceinline__ void each(F f) const {
+    for (int j = (int)(threadIdx.x & 63); j < n; j += 64) f(id[j], v[j]);
+  }
+};
+
+// Wave-level radix select (same contract as radix_select): the composite of
+// the element at which the cumulative measure over kept candidates first
+// reaches target (0 < target <= total).
+template <int ORD, typename Meas>
+__device__ uint64_t wave_radix_select(const WaveCands& src, const Pred& pr, Meas meas, uint64_t target, MergeSmem& sm) {
+  const int lane = threadIdx.x & 63;
+  constexpr int PASSES = ORD == ORD_ID ? 2 : 5;
+  uint64_t prefix = 0;
+  for (int pass = 0; pass < PASSES; ++pass) {
+    const int shift = 10 * (PASSES - 1 - pass);
+    for (int i = lane; i < 1024; i += 64) sm.hist[i] = 0;
+    wave_sync();
+    src.each([&](int i, float l) {
+      if (!pr.keep(i, l)) return;
+      const uint64_t c = composite<ORD>(l, i);
+      if ((c >> (shift + 10)) != prefix) return;
+      const uint64_t w = meas(i, l);
+      if (w) atomicAdd((unsigned long long*)&sm.hist[(c >> shift) & 1023], (unsigned long long)w);
+    });
+    wave_sync();
+    // lane owns bins 1023-16*lane .. 1008-16*lane (descending)
+    uint64_t ls = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) ls += sm.hist[1023 - 16 * lane - q];
+    uint64_t incl = ls;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    uint64_t c = incl - ls;
+    if (c < target && incl >= target) {
+      for (int q = 0; q < 16; ++q) {
+        const uint64_t hv = sm.hist[1023 - 16 * lane - q];
+        if (c < target && c + hv >= target) {
+          sm.bc64[0] = (uint64_t)(1023 - 16 * lane - q);
+          sm.bc64[1] = c;
+        }
+        c += hv;
+      }
+    }
+    wave_sync();
+    prefix = (prefix << 10) | sm.bc64[0];
+    target -= sm.bc64[1];
+    wave_sync();
+  }
+  return prefix;
+}
+
+__global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) {
+  extern __shared__ __align__(16) char dyn[];
+  __shared__ ExactSmem esm;
+  __shared__ MergeSmem sm;
+  __shared__ int s_fallback;
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int G = P.G;
+  const RowParams rp = row_params(a, b, P.rule_cap);
+  if (tid < 64) {
+    const int lane = tid;
+    const SliceHdr* H = P.hdr + (long long)b * G;
+    // headers: lane s < G holds slice s
+    float hm = -INFINITY, htau = -INFINITY;
+    int hn = 0, hflag = 0, hbest = 0x7FFFFFFF;
+    if (lane < G) {
+      hm = H[lane].m;
+      hflag = H[lane].flags;
+      if (rp.rule == RULE_GREEDY) hbest = H[lane].best_i;
+      else if (rp.rule != RULE_ALL) { htau = H[lane].tau; hn = H[lane].n; }
+    }
+    const float m = wave_max(hm);
+    int fallback = (wave_sum_i(hflag) != 0 || rp.rule == RULE_ALL) ? 1 : 0;
+    if (rp.rule == RULE_GREEDY) {
+      const int cand = (lane < G && hm == m) ? hbest : 0x7FFFFFFF;
+      const int bi = wave_min_i(cand);
+      if (lane == 0) {
+        if (a.tokens) a.tokens[b] = bi;
+        if (a.kept) a.kept[b] = 1;
+        P.path[b] = 2;
+      }
+      fallback = 0;
+    } else if (!fallback) {
+      float tcov = htau;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) tcov = fmaxf(tcov, __shfl_xor(tcov, o, 64));
+      // candidate offsets (prefix over the first G lanes)
+      int off = hn;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(off, o, 64);
+        if (lane >= o) off += y;
+      }
+      const int N = __shfl(off, 63, 64);
+      off -= hn;
+      float* cv = (float*)dyn;
+      int* ci = (int*)(dyn + (size_t)G * P.cap * sizeof(float));
+      for (int s = 0; s < G; ++s) {
+        const int ns = __shfl(hn, s, 64), os = __shfl(off, s, 64);
+        const int2* src = P.cand + ((long long)b * G + s) * P.cap;
+        for (int j = lane; j < ns; j += 64) {
+          const int2 c = src[j];
+          cv[os + j] = __int_as_float(c.x);
+          ci[os + j] = c.y;
+        }
+      }
+      wave_sync();
+      const WaveCands src{cv, ci, N};
+      Pred pr = {0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
+      auto mass = [m](int, float l) { return exp_fix44(l - m); };
+      auto one = [](int, float) { return (uint64_t)1; };
+      auto count = [&](const Pred& p) {
+        int c = 0;
+        src.each([&](int i, float l) { c += p.keep(i, l) ? 1 : 0; });
+        return wave_sum_i(c);
+      };
+      auto msum = [&](const Pred& p) {
+        uint64_t z = 0;
+        src.each([&](int i, float l) { if (p.keep(i, l)) z += exp_fix44(l - m); });
+        return wave_sum_u64(z);
+      };
+      const float theta = (float)(1.0 - (double)rp.top_p);
+      bool ambiguous = false;
+
+      // Top-p with the normaliser Z = sum_i exp_fix44(l_i - m) known to lie in
+      // [Zlo, Zhi].  S is the alive mass: exact when s_exact, else Z itself.
+      auto apply_p = [&](bool s_exact) {
+        // per-slice bounds summed across lanes.  exp_fix44 has relative error
+        // <= (|t| + 2) 2^-23 (t = d log2 e, |t| < 90 where it is nonzero) and
+        // the float estimate <= 1e-5 (argument rounding, 1-ulp exp, float
+        // sums of < 2^7 terms): the 1e-4 factors and the per-element floor
+        // allowances make both bounds rigorous
+        double lo = 0.0, hi = 0.0;
+        if (lane < G && hm != -INFINITY) {
+          const SliceHdr& h = H[lane];
+          const double sc = exp((double)hm - (double)m);
+          const double z = (double)h.zlo;
+          lo = fmax(0.0, z * sc * (1.0 - 1e-4) - (double)h.ntier);
+          if (h.zf >= 0.0) {
+            hi = (h.zf * sc * (1.0 + 1e-4) + 1e-6) * 17592186044416.0 + (double)(h.ntier + h.nrest);
+          } else {
+            const double band = exp((double)h.zthr - (double)hm) * sc * 17592186044416.0 * (1.0 + 1e-4) + 1.0;
+            hi = z * sc * (1.0 + 1e-4) + (double)h.ntier + (double)h.nrest * band;
+          }
+        }
+        lo = wave_sum_f64(lo);
+        hi = wave_sum_f64(hi);
+        const uint64_t Zlo = (uint64_t)lo;
+        const uint64_t Zhi = hi >= 4.0e18 ? (1ull << 62) : (uint64_t)ceil(hi);
+        long long Rlo, Rhi;
+        if (s_exact) {
+          const long long S = (long long)msum(pr);
+          Rlo = S - (long long)floor_theta_z(theta, Zhi);
+          Rhi = S - (long long)floor_theta_z(theta, Zlo);
+        } else {
+          Rlo = (long long)(Zlo - floor_theta_z(theta, Zlo));
+          Rhi = (long long)(Zhi - floor_theta_z(theta, Zhi));
+        }
+        if (Rhi <= 0) { pr.none = 1; return; }
+        if (Rlo <= 0) { ambiguous = true; return; }
+        Pred pc = pr;
+        pc.cov = tcov;
+        const long long Scov = (long long)msum(pc);
+        if (Rlo > Scov) {
+          // every covered element survives; the kept set stays inside the
+          // covered region only if a later filter confines it there (the
+          // min-p cut is >= every slice threshold; the top-k set is covered)
+          if (rp.rule == RULE_P) ambiguous = true;
+          return;
+        }
+        if (Rhi > Scov) { ambiguous = true; return; }
+        const uint64_t clo = wave_radix_select<ORD_P>(src, pc, mass, (uint64_t)Rlo, sm);
+        const uint64_t chi = wave_radix_select<ORD_P>(src, pc, mass, (uint64_t)Rhi, sm);
+        if (clo != chi) { ambiguous = true; return; }
+        pr.use_p = 1;
+        pr.cp = clo;
+      };
+      auto apply_m = [&]() {
+        pr.use_m = 1;
+        pr.thr = m + min_p_log(a, rp.min_p);
+      };
+      if (a.chain == WH_CHAIN_MLX && rp.rule == RULE_K) {
+        // the candidates hold the whole top-k set (at least k of them)
+        if (rp.use_k) {
+          pr.ck = wave_radix_select<ORD_A>(src, pr, one, (uint64_t)rp.top_k, sm);
+          pr.use_k = 1;
+        }
+        if (rp.use_p) apply_p(rp.use_k);
+        if (!ambiguous && rp.use_m && !pr.none) apply_m();
+      } else if (a.chain == WH_CHAIN_MLX) {
+        // rule M or P: no top-p together with top-k here.  k -> min-p: the
+        // min-p set is a value prefix held by the candidates; with more than k
+        // members the row's first k (order A) are its first k, else top-k
+        // keeps all of it.
+        if (rp.use_p) apply_p(false);
+        if (!ambiguous && rp.use_m && !pr.none) apply_m();
+        if (!ambiguous && rp.use_k && !pr.none && count(pr) > rp.top_k) {
+          pr.ck = wave_radix_select<ORD_A>(src, pr, one, (uint64_t)rp.top_k, sm);
+          pr.use_k = 1;
+        }
+      } else {
+        if (rp.use_p) apply_p(false);
+        if (!ambiguous && rp.use_m && !pr.none) apply_m();
+        if (!ambiguous && rp.use_k && !pr.none && count(pr) > rp.top_k) {
+          pr.ck = wave_radix_select<ORD_A>(src, pr, one, (uint64_t)rp.top_k, sm);
+          pr.use_k = 1;
+        }
+      }
+      if (ambiguous) {
+        fallback = 1;
+      } else {
+        // Draw: integer inverse CDF in vocabulary order over the kept candidates.
+        const float invT = (float)(1.0 / (double)rp.T);
+        const float Tc = (float)fmax((double)rp.T, 1e-5);
+        auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, Tc)); };
+        uint64_t zv = 0;
+        int nk = 0;
+        src.each([&](int i, float l) {
+          if (pr.keep(i, l)) { zv += vw(i, l); ++nk; }
+        });
+        const uint64_t ZV = wave_sum_u64(zv);
+        const int nkept = wave_sum_i(nk);
+        if (a.tokens) {
+          int tok = 0;
+          if (ZV) {
+            const uint64_t tgt = draw_target(a.u[b], ZV);
+            tok = 0x3FFFF - (int)wave_radix_select<ORD_ID>(src, pr, vw, tgt + 1, sm);
+          }
+          if (lane == 0) a.tokens[b] = tok;
+        }
+        if (lane == 0) {
+          if (a.kept) a.kept[b] = nkept;
+          P.path[b] = 0;
+        }
+        float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
+        if (out) {
+          const double lz = log(ldexp((double)ZV, -44));
+          src.each([&](int i, float l) {
+            if (!pr.keep(i, l)) return;
+            out[i] = a.out_mode == WH_OUT_MASKED ? l : (float)((double)chain_scale(a.chain, l - m, invT, Tc) - lz);
+          });
+        }
+      }
+    }
+    if (lane == 0) s_fallback = fallback;
+  }
   __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(&P.counters[b], 1) == P.G - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  finalize_row(a, P, b, rule, T, top_p, min_p, top_k, use_k, use_p, use_m, dyn, sm);
+  if (s_fallback) {
+    if (tid == 0) P.path[b] = 1;
+    exact_row(a, b, dyn, esm);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -537,25 +692,26 @@ static HostPlan make_plan(int B, int V, int dtype) {
   HostPlan p;
   p.ept = dtype == WH_DTYPE_BF16 ? 8 : 4;
   const int slmax = FT * p.ept * FAST_RMAX;
-  int g = std::max((512 + B - 1) / std::max(B, 1), (V + slmax - 1) / slmax);
-  g = std::min(g, 8);
+  int g = std::max((256 + B - 1) / std::max(B, 1), (V + slmax - 1) / slmax);
+  g = std::min(g, 32);
   p.G = g;
   int sl = (V + g - 1) / g;
   sl = (sl + p.ept - 1) / p.ept * p.ept;
   p.SL = sl;
   p.R = (sl + FT * p.ept - 1) / (FT * p.ept);
-  p.cap = std::min(2048, 8192 / g);
+  p.cap = std::min(2048, 16384 / g);
   p.rule_cap = p.cap / 2;
   return p;
 }
 
 struct WsLayout {
-  size_t counters, hdr, cand, total;
+  size_t path, hdr, cand, total;
 };
 
+// Workspace: [path B x int32][slice headers B*G][candidates B*G*cap]
 static WsLayout ws_layout(int B, const HostPlan& p) {
   WsLayout w;
-  w.counters = 0;
+  w.path = 0;
   w.hdr = ((size_t)B * 4 + 255) / 256 * 256;
   w.cand = w.hdr + (size_t)B * p.G * sizeof(SliceHdr);
   w.total = w.cand + (size_t)B * p.G * p.cap * sizeof(int2);
@@ -564,31 +720,40 @@ static WsLayout ws_layout(int B, const HostPlan& p) {
 
 size_t sample_workspace_bytes(int B, int V) {
   if (B <= 0 || V <= 0) return 256;
-  // the larger of the two element widths' plans
   WsLayout a = ws_layout(B, make_plan(B, V, WH_DTYPE_F32));
   WsLayout b = ws_layout(B, make_plan(B, V, WH_DTYPE_BF16));
   return std::max(a.total, b.total);
 }
 
-template <int DT, int R>
-static void launch_fast_t(const SampleKArgs& k, const FastPlan& fp, int grid, size_t lds, hipStream_t st) {
-  auto fn = sample_fast_kernel<DT, R>;
-  if (lds > 65536) hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  hipLaunchKernelGGL(fn, dim3(grid), dim3(FT), lds, st, k, fp);
+static int set_lds(const void* fn, size_t lds) {
+  if (lds <= 65536) return WH_OK;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return fail(WH_EHIP, "hipFuncSetAttribute(%zu bytes LDS) failed: %s", lds, hipGetErrorString(e));
+  return WH_OK;
 }
 
+template <int DT, int R>
+static int launch_slice_t(const SampleKArgs& k, const FastPlan& fp, size_t lds, hipStream_t st) {
+  auto fn = slice_kernel<DT, R>;
+  int rc = set_lds((const void*)fn, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(fn, dim3(k.B * fp.G), dim3(FT), lds, st, k, fp);
+  return WH_OK;
+}
+
+// R is rounded up to an instantiated register count.
 template <int DT>
-static void launch_fast_dt(int R, const SampleKArgs& k, const FastPlan& fp, int grid, size_t lds, hipStream_t st) {
-  switch (R) {
-    case 1: launch_fast_t<DT, 1>(k, fp, grid, lds, st); break;
-    case 2: launch_fast_t<DT, 2>(k, fp, grid, lds, st); break;
-    case 3: launch_fast_t<DT, 3>(k, fp, grid, lds, st); break;
-    case 4: launch_fast_t<DT, 4>(k, fp, grid, lds, st); break;
-    case 5: launch_fast_t<DT, 5>(k, fp, grid, lds, st); break;
-    case 6: launch_fast_t<DT, 6>(k, fp, grid, lds, st); break;
-    case 7: launch_fast_t<DT, 7>(k, fp, grid, lds, st); break;
-    default: launch_fast_t<DT, 8>(k, fp, grid, lds, st); break;
-  }
+static int launch_slice_dt(int R, const SampleKArgs& k, const FastPlan& fp, size_t lds, hipStream_t st) {
+  if (R <= 1) return launch_slice_t<DT, 1>(k, fp, lds, st);
+  if (R <= 2) return launch_slice_t<DT, 2>(k, fp, lds, st);
+  if (R <= 3) return launch_slice_t<DT, 3>(k, fp, lds, st);
+  if (R <= 4) return launch_slice_t<DT, 4>(k, fp, lds, st);
+  if (R <= 5) return launch_slice_t<DT, 5>(k, fp, lds, st);
+  if (R <= 6) return launch_slice_t<DT, 6>(k, fp, lds, st);
+  if (R <= 8) return launch_slice_t<DT, 8>(k, fp, lds, st);
+  if (R <= 10) return launch_slice_t<DT, 10>(k, fp, lds, st);
+  if (R <= 12) return launch_slice_t<DT, 12>(k, fp, lds, st);
+  return launch_slice_t<DT, 16>(k, fp, lds, st);
 }
 
 int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st) {
@@ -604,20 +769,21 @@ int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st
   fp.cap = hp.cap;
   fp.rule_cap = hp.rule_cap;
   char* ws = (char*)p->workspace;
-  fp.counters = (int*)(ws + wl.counters);
+  fp.path = (int*)(ws + wl.path);
   fp.hdr = (SliceHdr*)(ws + wl.hdr);
   fp.cand = (int2*)(ws + wl.cand);
-  // dynamic LDS: slice phase (hash + slice bitmap + candidate buffer), merge
-  // phase (G * cap candidates), exact fallback (hash + row bitmap)
-  const size_t slice = cand_buf_offset(k.hcap, hp.SL) + (size_t)hp.cap * sizeof(int2);
-  const size_t merge = (size_t)hp.G * hp.cap * 8;
-  const size_t exact = penalty_lds_bytes(k);
-  const size_t lds = std::max(slice, std::max(merge, exact));
-  const int grid = (k.B + 7) / 8 * 8 * hp.G;
-  if (k.dtype == WH_DTYPE_BF16) launch_fast_dt<1>(hp.R, k, fp, grid, lds, st);
-  else launch_fast_dt<0>(hp.R, k, fp, grid, lds, st);
+  const size_t lds_slice = cand_buf_offset(k.hcap, hp.SL) + (size_t)hp.cap * sizeof(int2);
+  const size_t lds_merge = std::max((size_t)hp.G * hp.cap * 8, penalty_lds_bytes(k));
+  int rc = k.dtype == WH_DTYPE_BF16 ? launch_slice_dt<1>(hp.R, k, fp, lds_slice, st)
+                                    : launch_slice_dt<0>(hp.R, k, fp, lds_slice, st);
+  if (rc) return rc;
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(WH_EHIP, "sample_fast_kernel launch failed: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return fail(WH_EHIP, "slice_kernel launch failed: %s", hipGetErrorString(e));
+  rc = set_lds((const void*)merge_kernel, lds_merge);
+  if (rc) return rc;
+  hipLaunchKernelGGL(merge_kernel, dim3(k.B), dim3(1024), lds_merge, st, k, fp);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(WH_EHIP, "merge_kernel launch failed: %s", hipGetErrorString(e));
   return WH_OK;
 }
 

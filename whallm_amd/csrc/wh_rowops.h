@@ -198,7 +198,7 @@ __device__ __forceinline__ float chain_scale(int chain, float d, float invT, flo
 }
 
 // The whole exact algorithm for row b by one 1024-thread workgroup.
-__device__ void exact_row(const SampleKArgs& a, int b, char* dyn_smem, ExactSmem& sm) {
+__device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_smem, ExactSmem& sm) {
   const int tid = threadIdx.x, nt = blockDim.x;
   const int V = a.V;
   RowCtx rc;

@@ -169,7 +169,10 @@ extern "C" int wh_sample(const wh_sample_args* args, void* stream) {
 
 int wh::launch_sample_exact(const SampleKArgs& k, hipStream_t st) {
   size_t lds = penalty_lds_bytes(k);
-  if (lds > 65536) hipFuncSetAttribute((const void*)sample_exact_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void*)sample_exact_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return fail(WH_EHIP, "hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+  }
   hipLaunchKernelGGL(sample_exact_kernel, dim3(k.B), dim3(1024), lds, st, k);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "sample_exact_kernel launch failed: %s", hipGetErrorString(e));
@@ -182,8 +185,11 @@ extern "C" int wh_apply_penalties(const wh_sample_args* args, void* stream) {
   int rc = prepare_sample(args, &k, false);
   if (rc) return rc;
   if (k.hcap == 0 || k.B == 0) return WH_OK;
-  if (penalty_lds_bytes(k) > 65536)
-    hipFuncSetAttribute((const void*)penalties_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)penalty_lds_bytes(k));
+  if (penalty_lds_bytes(k) > 65536) {
+    hipError_t e = hipFuncSetAttribute((const void*)penalties_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)penalty_lds_bytes(k));
+    if (e != hipSuccess) return fail(WH_EHIP, "hipFuncSetAttribute failed: %s", hipGetErrorString(e));
+  }
   hipLaunchKernelGGL(penalties_kernel, dim3(k.B), dim3(1024), penalty_lds_bytes(k), (hipStream_t)stream, k);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "penalties_kernel launch failed: %s", hipGetErrorString(e));

@@ -161,6 +161,14 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
     return tokens if len(res) == 1 else tuple(res)
 
 
+def last_paths(device, B: int) -> torch.Tensor:
+    """Per-row engine path of the last sliced-engine call on the current
+    stream's workspace: 0 merged from candidates, 1 exact fallback, 2 greedy
+    (diagnostics; the row results are identical either way)."""
+    ws = L.workspace(torch.device(device), 0)
+    return ws[:4 * B].view(torch.int32).clone()
+
+
 def filter_rows(logits: torch.Tensor, *, chain="whallm", temperature: float = 1.0, top_p: float = 1.0,
                 top_k: int = 0, min_p: float = 0.0, out_mode: int = L.OUT_LOGPROBS,
                 history=None, history_len=None, repetition_penalty: float = 0.0, presence_penalty: float = 0.0,
