@@ -38,17 +38,16 @@ constexpr float ZBAND = 8.0f;     // exact-mass band below the slice max, nats
 enum { RULE_GREEDY = 0, RULE_M = 1, RULE_K = 2, RULE_P = 3, RULE_ALL = 4 };
 
 struct SliceHdr {
-  float m;            // slice max (penalised)
-  float tau;          // every slice element >= tau is a candidate
-  int n;              // candidates written
-  int flags;          // 1: overflow / rule ALL -- the row needs the exact engine
-  unsigned long long zlo;  // sum of exp_fix44(l - m) over l >= zthr (exact)
-  float zthr;         // band floor for zlo
-  int ntier;          // elements in the band
-  int nrest;          // elements below the band
-  int best_i;         // greedy: lowest index attaining the max
-  double zf;          // sum of exp(l - m) over the slice (hardware exp), < 0 if not computed
-  int pad[4];
+  float m;       // slice max (penalised)
+  float tau;     // every slice element >= tau is a candidate
+  int n;         // candidates written (= elements >= tau unless flags)
+  int flags;     // 1: overflow / rule ALL -- the row needs the exact engine
+  float t[3];    // band floors t1 >= t2 >= t3, all <= tau
+  int c[3];      // elements >= t1, >= t2, >= t3 (cumulative, include candidates)
+  int nall;      // elements in the slice
+  int best_i;    // greedy: lowest index attaining the max
+  double zf;     // sum of exp(l - m) over the slice (hardware exp), < 0 if not computed
+  int pad[2];
 };
 static_assert(sizeof(SliceHdr) == 64, "SliceHdr layout");
 
@@ -57,7 +56,8 @@ struct FastPlan {
   int SL;         // slice length (multiple of the elements per 16-byte load)
   int cap;        // candidate capacity per slice
   int rule_cap;   // largest k (or top-p window) a slice may bound
-  int* path;      // [B] 0: merged from candidates, 1: exact engine, 2: greedy
+  int* path;      // [B] 0: merged from candidates, 1: exact engine (overflow / no filter),
+                  //     2: greedy, 3: exact engine (top-p cut not settled by the bounds)
   SliceHdr* hdr;  // [B * G]
   int2* cand;     // [B * G * cap] (value bits, id)
 };
@@ -223,7 +223,9 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
 
   // 2. penalties: history window -> LDS hash of the slice's tokens; the owner
   //    of each penalised element computes its value from the register copy,
-  //    stores it in the hash and writes -inf into the register slot
+  //    stores it in the hash and writes -inf into the register slot.  The
+  //    history row (up to 4 ids per thread) and its length are fetched with
+  //    the logits, so their latency overlaps.
   const int hcap = a.hcap;
   int32_t* hkeys = (int32_t*)dyn;
   int32_t* hpos = hkeys + hcap;
@@ -231,23 +233,30 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   uint32_t* bm = (uint32_t*)(hcnt + hcap);
   float* hval = (float*)hpos;
   if (hcap > 0) {
+    constexpr int HPF = 4;
+    const int32_t* h = a.hist + (long long)b * a.hist_stride;
+    const int hs = (int)a.hist_stride;
+    const bool pf = hs <= HPF * FT;
+    int hreg[HPF];
+#pragma unroll
+    for (int q = 0; q < HPF; ++q) {
+      const int j = tid + q * FT;
+      hreg[q] = (pf && j < hs) ? h[j] : -1;
+    }
+    int len = a.hist_len ? a.hist_len[b] : 0;
     const int words = (v1 - v0 + 31) >> 5;
     for (int t = tid; t < hcap; t += FT) { hkeys[t] = -1; hpos[t] = -1; hcnt[t] = 0; }
     for (int w = tid; w < words; w += FT) bm[w] = 0u;
-    int len = a.hist_len ? a.hist_len[b] : 0;
-    len = max(0, min(len, (int)a.hist_stride));
+    len = max(0, min(len, hs));
     const bool on_r = a.rep != 0.0f, on_p = a.pres != 0.0f, on_f = a.freq != 0.0f;
     auto window = [len](int ctx) { return (ctx <= 0 || ctx > len) ? len : ctx; };
     const int wr = on_r ? window(a.rep_ctx) : 0;
     const int wp = on_p ? window(a.pres_ctx) : 0;
     const int wf = on_f ? window(a.freq_ctx) : 0;
     const int W = max(wr, max(wp, wf));
-    const int32_t* h = a.hist + (long long)b * a.hist_stride;
-    __syncthreads();
     const int hshift = 32 - a.hlog2, hmask = hcap - 1;
-    for (int j = len - W + tid; j < len; j += FT) {
-      const int t = h[j];
-      if (t < v0 || t >= v1) continue;
+    auto insert = [&](int j, int t) {
+      if (t < v0 || t >= v1) return;
       uint32_t q = ((uint32_t)t * 2654435761u) >> hshift;
       while (true) {
         const int old = atomicCAS(&hkeys[q], -1, t);
@@ -257,6 +266,16 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
       atomicMax(&hpos[q], j);
       if (j >= len - wf) atomicAdd(&hcnt[q], 1);
       atomicOr(&bm[(t - v0) >> 5], 1u << ((t - v0) & 31));
+    };
+    __syncthreads();
+    if (pf) {
+#pragma unroll
+      for (int q = 0; q < HPF; ++q) {
+        const int j = tid + q * FT;
+        if (j >= len - W && j < len) insert(j, hreg[q]);
+      }
+    } else {
+      for (int j = len - W + tid; j < len; j += FT) insert(j, h[j]);
     }
     __syncthreads();
 #pragma unroll
@@ -291,8 +310,12 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
       if (i >= 0) f(i, hval[j]);
     }
   };
+  auto killed_bits = [&](int g) -> uint32_t {
+    return hcap > 0 ? (bm[(g - v0) >> 5] >> ((g - v0) & 31)) & ((1u << EPT) - 1u) : 0u;
+  };
 
   // 3. slice max and, for greedy rows, the lowest index attaining it
+  const bool greedy = rp.rule == RULE_GREEDY;
   float mx = -INFINITY;
   int mi = 0x7FFFFFFF;
 #pragma unroll
@@ -302,16 +325,24 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         const float l = grp_elem<DT>(d[r], e);
-        if (mi == 0x7FFFFFFF || l > mx) { mx = l; mi = g + e; }
+        if (greedy) {
+          if (mi == 0x7FFFFFFF || l > mx) { mx = l; mi = g + e; }
+        } else {
+          mx = fmaxf(mx, l);
+        }
       }
     }
   }
   each_pen([&](int i, float l) {
-    if (mi == 0x7FFFFFFF || l > mx || (l == mx && i < mi)) { mx = l; mi = i; }
+    if (greedy) {
+      if (mi == 0x7FFFFFFF || l > mx || (l == mx && i < mi)) { mx = l; mi = i; }
+    } else {
+      mx = fmaxf(mx, l);
+    }
   });
   const float ms = block_reduce(mx, sm.sf, OpMaxF(), -INFINITY);
 
-  if (rp.rule == RULE_GREEDY) {
+  if (greedy) {
     const int cand = (mi != 0x7FFFFFFF && mx == ms) ? mi : 0x7FFFFFFF;
     const int bi = block_reduce(cand, sm.si, OpMinI(), 0x7FFFFFFF);
     if (out) {  // Whallm's sampling_logprobs returns the (penalised) logits at T == 0
@@ -335,48 +366,70 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     return;
   }
 
-  // 4. candidate threshold and the exact-mass band
+  // 4. candidate threshold and the band thresholds below it
   float tau;
   if (rp.rule == RULE_M) tau = ms + min_p_log(a, rp.min_p);
   else tau = slice_kth<DT, R>(d, v0, v1, hkeys, hval, hcap, rp.rule == RULE_K ? rp.top_k : P.rule_cap, sm);
-  const float zthr = fminf(tau, ms - ZBAND);
+  const float t1 = fminf(tau, ms - 4.5f), t2 = fminf(t1, ms - 6.0f), t3 = fminf(t2, ms - 8.0f);
   const bool need_zf = rp.use_p && !rp.use_m;
 
-  // 5. one pass: candidates to LDS, band mass, optional float estimate
+  // 5. one pass: candidates (wave-aggregated appends to LDS), band counts
+  //    (wave ballots), optional hardware-exp estimate of sum exp(l - ms)
   int2* buf = (int2*)(dyn + cand_buf_offset(hcap, P.SL));
   if (tid == 0) sm.cnt = 0;
   __syncthreads();
-  uint64_t zl = 0;
-  int ntier = 0, nall = 0;
+  const int lane = tid & 63;
+  int c1 = 0, c2 = 0, c3 = 0, nall = 0;  // c*: wave-uniform ballot counts
   float zs = 0.0f;
-  auto visit = [&](int i, float l) {
-    ++nall;
-    if (l >= zthr) {
-      if (l >= tau) {
-        const int slot = atomicAdd(&sm.cnt, 1);
-        if (slot < P.cap) buf[slot] = make_int2(__float_as_int(l), i);
-      }
-      ++ntier;
-      zl += exp_fix44(l - ms);
-    }
-    if (need_zf) zs += __expf(l - ms);
-  };
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int g = v0 + (r * FT + tid) * EPT;
-    if (g < v1) {
-      // penalised elements are visited once, through the hash, below
-      const uint32_t killed = hcap > 0 ? (bm[(g - v0) >> 5] >> ((g - v0) & 31)) & ((1u << EPT) - 1u) : 0u;
+    const bool in = g < v1;
+    const uint32_t killed = in ? killed_bits(g) : 0xFFu;
 #pragma unroll
-      for (int e = 0; e < EPT; ++e)
-        if (!((killed >> e) & 1u)) visit(g + e, grp_elem<DT>(d[r], e));
+    for (int e = 0; e < EPT; ++e) {
+      const float l = grp_elem<DT>(d[r], e);
+      const bool valid = in && !((killed >> e) & 1u);
+      nall += valid ? 1 : 0;
+      const uint64_t mk = __ballot(valid && l >= tau);
+      if (mk) {
+        int base = 0;
+        if (lane == 0) base = atomicAdd(&sm.cnt, (int)__popcll(mk));
+        base = __shfl(base, 0, 64);
+        if (valid && l >= tau) {
+          const int slot = base + (int)__popcll(mk & ((1ull << lane) - 1ull));
+          if (slot < P.cap) buf[slot] = make_int2(__float_as_int(l), g + e);
+        }
+      }
+      c1 += (int)__popcll(__ballot(valid && l >= t1));
+      c2 += (int)__popcll(__ballot(valid && l >= t2));
+      c3 += (int)__popcll(__ballot(valid && l >= t3));
+      if (need_zf && valid) zs += __expf(l - ms);
     }
   }
-  each_pen([&](int i, float l) { visit(i, l); });
-  const uint64_t zlo = block_reduce(zl, sm.s64, OpSumU64(), (uint64_t)0);
-  const int ntier_b = block_reduce(ntier, sm.si, OpSumI(), 0);
-  const int nall_b = block_reduce(nall, sm.si, OpSumI(), 0);
-  const double zf = need_zf ? block_reduce((double)zs, sm.sd, OpSumF64(), 0.0) : -1.0;
+  int p1 = 0, p2 = 0, p3 = 0;
+  each_pen([&](int i, float l) {
+    ++nall;
+    if (l >= tau) {
+      const int slot = atomicAdd(&sm.cnt, 1);
+      if (slot < P.cap) buf[slot] = make_int2(__float_as_int(l), i);
+    }
+    p1 += l >= t1;
+    p2 += l >= t2;
+    p3 += l >= t3;
+    if (need_zf) zs += __expf(l - ms);
+  });
+  // one combined block reduction
+  const int wv = tid >> 6;
+  int q1 = wave_sum_i(p1) + c1, q2 = wave_sum_i(p2) + c2, q3 = wave_sum_i(p3) + c3, qa = wave_sum_i(nall);
+  const double qz = need_zf ? wave_sum_f64((double)zs) : 0.0;
+  if (lane == 0) {
+    sm.si[wv] = q1;
+    ((int*)sm.s64)[wv] = q2;
+    ((int*)sm.s64)[16 + wv] = q3;
+    sm.sf[wv] = __int_as_float(qa);
+    sm.sd[wv] = qz;
+  }
   __syncthreads();
   const int n = sm.cnt;
   const int nw = min(n, P.cap);
@@ -394,15 +447,28 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     }
   }
   if (tid == 0) {
+    int s1 = 0, s2 = 0, s3 = 0, sa = 0;
+    double sz = 0.0;
+    const int nwv = FT / 64;
+    for (int w = 0; w < nwv; ++w) {
+      s1 += sm.si[w];
+      s2 += ((int*)sm.s64)[w];
+      s3 += ((int*)sm.s64)[16 + w];
+      sa += __float_as_int(sm.sf[w]);
+      sz += sm.sd[w];
+    }
     hdr->m = ms;
     hdr->tau = tau;
     hdr->n = nw;
     hdr->flags = n > P.cap ? 1 : 0;
-    hdr->zlo = zlo;
-    hdr->zthr = zthr;
-    hdr->ntier = ntier_b;
-    hdr->nrest = nall_b - ntier_b;
-    hdr->zf = zf;
+    hdr->t[0] = t1;
+    hdr->t[1] = t2;
+    hdr->t[2] = t3;
+    hdr->c[0] = s1;
+    hdr->c[1] = s2;
+    hdr->c[2] = s3;
+    hdr->nall = sa;
+    hdr->zf = need_zf ? sz : -1.0;
   }
 }
 
@@ -435,8 +501,28 @@ struct WaveCands {
 template <int ORD, typename Meas>
 __device__ uint64_t wave_radix_select(const WaveCands& src, const Pred& pr, Meas meas, uint64_t target, MergeSmem& sm) {
   const int lane = threadIdx.x & 63;
-  constexpr int PASSES = ORD == ORD_ID ? 2 : 5;
-  uint64_t prefix = 0;
+  // Bits above the highest bit in which two kept composites differ are
+  // common to all of them: start the 10-bit digits below it, so the first
+  // pass spreads the candidates over the bins instead of piling them into
+  // one (LDS atomics on one address serialise).
+  uint64_t cmin = ~0ull, cmax = 0;
+  src.each([&](int i, float l) {
+    if (!pr.keep(i, l)) return;
+    const uint64_t c = composite<ORD>(l, i);
+    cmin = c < cmin ? c : cmin;
+    cmax = c > cmax ? c : cmax;
+  });
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint64_t a = __shfl_xor(cmin, o, 64), b = __shfl_xor(cmax, o, 64);
+    cmin = a < cmin ? a : cmin;
+    cmax = b > cmax ? b : cmax;
+  }
+  if (cmax < cmin) return 0;  // nothing kept (callers never ask)
+  const uint64_t diff = cmin ^ cmax;
+  const int top = diff ? 64 - __clzll((long long)diff) : 1;  // bits that vary
+  const int PASSES = (top + 9) / 10;
+  uint64_t prefix = cmax >> (10 * PASSES);
   for (int pass = 0; pass < PASSES; ++pass) {
     const int shift = 10 * (PASSES - 1 - pass);
     for (int i = lane; i < 1024; i += 64) sm.hist[i] = 0;
@@ -483,6 +569,7 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
   __shared__ ExactSmem esm;
   __shared__ MergeSmem sm;
   __shared__ int s_fallback;
+  constexpr int SPEC = 64;  // candidates per slice fetched together with the headers
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int G = P.G;
@@ -490,19 +577,26 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
   if (tid < 64) {
     const int lane = tid;
     const SliceHdr* H = P.hdr + (long long)b * G;
-    // headers: lane s < G holds slice s
-    float hm = -INFINITY, htau = -INFINITY;
-    int hn = 0, hflag = 0, hbest = 0x7FFFFFFF;
-    if (lane < G) {
-      hm = H[lane].m;
-      hflag = H[lane].flags;
-      if (rp.rule == RULE_GREEDY) hbest = H[lane].best_i;
-      else if (rp.rule != RULE_ALL) { htau = H[lane].tau; hn = H[lane].n; }
+    // one round trip: headers (lane s < G), the row's uniform, and the first
+    // SPEC candidates of every slice
+    SliceHdr hd;
+    if (lane < G) hd = H[lane];
+    const float ub = (a.tokens && rp.rule != RULE_GREEDY) ? a.u[b] : 0.0f;
+    float* cv = (float*)dyn;
+    int* ci = (int*)(dyn + (size_t)G * P.cap * sizeof(float));
+    int2 spec[4];
+    const bool spec_ok = G <= 4 && rp.rule != RULE_GREEDY && rp.rule != RULE_ALL;
+    if (spec_ok) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        if (s < G) spec[s] = P.cand[((long long)b * G + s) * P.cap + lane];
     }
+    const float hm = lane < G ? hd.m : -INFINITY;
+    const int hflag = lane < G ? hd.flags : 0;
     const float m = wave_max(hm);
     int fallback = (wave_sum_i(hflag) != 0 || rp.rule == RULE_ALL) ? 1 : 0;
     if (rp.rule == RULE_GREEDY) {
-      const int cand = (lane < G && hm == m) ? hbest : 0x7FFFFFFF;
+      const int cand = (lane < G && hm == m) ? hd.best_i : 0x7FFFFFFF;
       const int bi = wave_min_i(cand);
       if (lane == 0) {
         if (a.tokens) a.tokens[b] = bi;
@@ -511,7 +605,8 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
       }
       fallback = 0;
     } else if (!fallback) {
-      float tcov = htau;
+      const int hn = lane < G ? hd.n : 0;
+      float tcov = lane < G ? hd.tau : -INFINITY;
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) tcov = fmaxf(tcov, __shfl_xor(tcov, o, 64));
       // candidate offsets (prefix over the first G lanes)
@@ -523,12 +618,19 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
       }
       const int N = __shfl(off, 63, 64);
       off -= hn;
-      float* cv = (float*)dyn;
-      int* ci = (int*)(dyn + (size_t)G * P.cap * sizeof(float));
       for (int s = 0; s < G; ++s) {
         const int ns = __shfl(hn, s, 64), os = __shfl(off, s, 64);
         const int2* src = P.cand + ((long long)b * G + s) * P.cap;
-        for (int j = lane; j < ns; j += 64) {
+        int j0 = 0;
+        if (spec_ok) {
+          int2 c = spec[0];
+          if (s == 1) c = spec[1];
+          if (s == 2) c = spec[2];
+          if (s == 3) c = spec[3];
+          if (lane < ns) { cv[os + lane] = __int_as_float(c.x); ci[os + lane] = c.y; }
+          j0 = SPEC;
+        }
+        for (int j = j0 + lane; j < ns; j += 64) {
           const int2 c = src[j];
           cv[os + j] = __int_as_float(c.x);
           ci[os + j] = c.y;
@@ -555,26 +657,37 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
       // Top-p with the normaliser Z = sum_i exp_fix44(l_i - m) known to lie in
       // [Zlo, Zhi].  S is the alive mass: exact when s_exact, else Z itself.
       auto apply_p = [&](bool s_exact) {
-        // per-slice bounds summed across lanes.  exp_fix44 has relative error
-        // <= (|t| + 2) 2^-23 (t = d log2 e, |t| < 90 where it is nonzero) and
-        // the float estimate <= 1e-5 (argument rounding, 1-ulp exp, float
-        // sums of < 2^7 terms): the 1e-4 factors and the per-element floor
-        // allowances make both bounds rigorous
+        // The candidates contribute their exact masses.  An element below the
+        // candidate cut but at or above band floor t_j (counted by the slice)
+        // has exp_fix44(l - m) >= floor(2^44 e^(t_j - m) (1 - eps)) - 1 and
+        // <= 2^44 e^(t_(j-1) - m) (1 + eps) + 1 (t_0 = tau), with eps = 1e-4
+        // well above exp_fix44's relative error (|t| + 2) 2^-23 for the
+        // arguments that matter; below t3 only the upper bound counts.  With
+        // a float estimate zf (hardware exp, error < 1e-5 including float
+        // sums of < 2^7 terms) the upper bound is zf-based instead.
+        const double SC = 17592186044416.0;
+        const uint64_t Scand = msum(Pred{0, 0, 0, 0, 0, 0, 0.0f, -INFINITY});
         double lo = 0.0, hi = 0.0;
-        if (lane < G && hm != -INFINITY) {
-          const SliceHdr& h = H[lane];
-          const double sc = exp((double)hm - (double)m);
-          const double z = (double)h.zlo;
-          lo = fmax(0.0, z * sc * (1.0 - 1e-4) - (double)h.ntier);
-          if (h.zf >= 0.0) {
-            hi = (h.zf * sc * (1.0 + 1e-4) + 1e-6) * 17592186044416.0 + (double)(h.ntier + h.nrest);
-          } else {
-            const double band = exp((double)h.zthr - (double)hm) * sc * 17592186044416.0 * (1.0 + 1e-4) + 1.0;
-            hi = z * sc * (1.0 + 1e-4) + (double)h.ntier + (double)h.nrest * band;
+        if (lane < G && hd.m != -INFINITY) {
+          const double fl[4] = {(double)hd.tau, (double)hd.t[0], (double)hd.t[1], (double)hd.t[2]};
+          const int cum[4] = {hd.n, hd.c[0], hd.c[1], hd.c[2]};
+          for (int j = 1; j < 4; ++j) {
+            const double cnt = (double)(cum[j] - cum[j - 1]);
+            if (cnt <= 0.0) continue;
+            const double wl = floor(exp(fl[j] - (double)m) * SC * (1.0 - 1e-4)) - 1.0;
+            lo += cnt * fmax(wl, 0.0);
+            hi += cnt * (exp(fl[j - 1] - (double)m) * SC * (1.0 + 1e-4) + 1.0);
           }
+          hi += (double)(hd.nall - hd.c[2]) * (exp(fl[3] - (double)m) * SC * (1.0 + 1e-4) + 1.0);
+          if (hd.zf >= 0.0) hi = -1.0;  // replaced below
         }
-        lo = wave_sum_f64(lo);
-        hi = wave_sum_f64(hi);
+        lo = wave_sum_f64(lo) + (double)Scand;
+        bool use_zf = wave_sum_i(lane < G && hd.m != -INFINITY && hd.zf >= 0.0 ? 1 : 0) > 0;
+        double zfh = 0.0;
+        if (lane < G && hd.m != -INFINITY && hd.zf >= 0.0)
+          zfh = hd.zf * exp((double)hd.m - (double)m) * (1.0 + 1e-4) * SC + (double)hd.nall + 1e-6 * SC;
+        if (use_zf) hi = wave_sum_f64(zfh);
+        else hi = wave_sum_f64(hi) + (double)Scand;
         const uint64_t Zlo = (uint64_t)lo;
         const uint64_t Zhi = hi >= 4.0e18 ? (1ull << 62) : (uint64_t)ceil(hi);
         long long Rlo, Rhi;
@@ -637,7 +750,7 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
         }
       }
       if (ambiguous) {
-        fallback = 1;
+        fallback = 3;
       } else {
         // Draw: integer inverse CDF in vocabulary order over the kept candidates.
         const float invT = (float)(1.0 / (double)rp.T);
@@ -653,7 +766,7 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
         if (a.tokens) {
           int tok = 0;
           if (ZV) {
-            const uint64_t tgt = draw_target(a.u[b], ZV);
+            const uint64_t tgt = draw_target(ub, ZV);
             tok = 0x3FFFF - (int)wave_radix_select<ORD_ID>(src, pr, vw, tgt + 1, sm);
           }
           if (lane == 0) a.tokens[b] = tok;
@@ -676,7 +789,7 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
   }
   __syncthreads();
   if (s_fallback) {
-    if (tid == 0) P.path[b] = 1;
+    if (tid == 0) P.path[b] = s_fallback == 3 ? 3 : 1;
     exact_row(a, b, dyn, esm);
   }
 }

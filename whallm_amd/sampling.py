@@ -163,8 +163,9 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
 
 def last_paths(device, B: int) -> torch.Tensor:
     """Per-row engine path of the last sliced-engine call on the current
-    stream's workspace: 0 merged from candidates, 1 exact fallback, 2 greedy
-    (diagnostics; the row results are identical either way)."""
+    stream's workspace: 0 merged from candidates, 1 exact engine (candidate
+    overflow or no filter), 2 greedy, 3 exact engine (top-p cut not settled
+    by the normaliser bounds).  Diagnostics only: results are identical."""
     ws = L.workspace(torch.device(device), 0)
     return ws[:4 * B].view(torch.int32).clone()
 
