@@ -121,6 +121,73 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return v;
 }
 
+// --------------------------------------------------------------------------
+// DPP wave reductions.  All 64 lanes must be active.  Four steps combine each
+// lane with a partner inside its row of 16 (quad_perm [1,0,3,2], quad_perm
+// [2,3,0,1], row_half_mirror, row_mirror), leaving every lane of a row with
+// the row's result; the four row results are read with v_readlane and
+// combined, so the value returned is wave uniform.  VALU latency only, no LDS.
+// --------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t lane_u32(uint32_t x, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)x, l); }
+__device__ __forceinline__ uint64_t lane_u64(uint64_t x, int l) {
+  return ((uint64_t)lane_u32((uint32_t)(x >> 32), l) << 32) | lane_u32((uint32_t)x, l);
+}
+template <typename Op>
+__device__ __forceinline__ uint32_t dpp_reduce_u32(uint32_t x, Op op) {
+  x = op(x, dpp32<0xB1>(x));
+  x = op(x, dpp32<0x4E>(x));
+  x = op(x, dpp32<0x141>(x));
+  x = op(x, dpp32<0x140>(x));
+  return op(op(lane_u32(x, 0), lane_u32(x, 16)), op(lane_u32(x, 32), lane_u32(x, 48)));
+}
+#define WH_DPP64_STEP(C)                                                                        \
+  {                                                                                             \
+    const uint64_t y_ = ((uint64_t)dpp32<C>((uint32_t)(x >> 32)) << 32) | dpp32<C>((uint32_t)x); \
+    x = op(x, y_);                                                                              \
+  }
+template <typename Op>
+__device__ __forceinline__ uint64_t dpp_reduce_u64(uint64_t x, Op op) {
+  WH_DPP64_STEP(0xB1)
+  WH_DPP64_STEP(0x4E)
+  WH_DPP64_STEP(0x141)
+  WH_DPP64_STEP(0x140)
+  return op(op(lane_u64(x, 0), lane_u64(x, 16)), op(lane_u64(x, 32), lane_u64(x, 48)));
+}
+#undef WH_DPP64_STEP
+__device__ __forceinline__ int wsum_i(int v) {
+  return (int)dpp_reduce_u32((uint32_t)v, [](uint32_t a, uint32_t b) { return a + b; });
+}
+__device__ __forceinline__ uint64_t wsum_u64(uint64_t v) {
+  return dpp_reduce_u64(v, [](uint64_t a, uint64_t b) { return a + b; });
+}
+__device__ __forceinline__ float wmax_f(float v) {
+  return __uint_as_float(
+      dpp_reduce_u32(__float_as_uint(v), [](uint32_t a, uint32_t b) { return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b))); }));
+}
+__device__ __forceinline__ int wmin_i(int v) {
+  return (int)dpp_reduce_u32((uint32_t)v, [](uint32_t a, uint32_t b) { return (uint32_t)min((int)a, (int)b); });
+}
+__device__ __forceinline__ int wmax_i(int v) {
+  return (int)dpp_reduce_u32((uint32_t)v, [](uint32_t a, uint32_t b) { return (uint32_t)max((int)a, (int)b); });
+}
+__device__ __forceinline__ uint32_t wmin_u32(uint32_t v) {
+  return dpp_reduce_u32(v, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wmax_u32(uint32_t v) {
+  return dpp_reduce_u32(v, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ double wsum_f64(double v) {
+  return __longlong_as_double((long long)dpp_reduce_u64((uint64_t)__double_as_longlong(v), [](uint64_t a, uint64_t b) {
+    return (uint64_t)__double_as_longlong(__longlong_as_double((long long)a) + __longlong_as_double((long long)b));
+  }));
+}
+// Number of lanes (of the active ones) where p holds; wave uniform.
+__device__ __forceinline__ int ballot_count(bool p) { return (int)__popcll(__ballot(p)); }
+
 // Reductions across the block through a 16-slot LDS scratch (one per wave).
 template <typename T, typename Op>
 __device__ __forceinline__ T block_reduce(T v, T* scratch, Op op, T ident) {

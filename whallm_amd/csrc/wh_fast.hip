@@ -1,93 +1,159 @@
 // wh_fast.hip -- the sliced single-read sampler engine for gfx950.
 //
-// Two kernels per call.
+// Two kernels per call and no synchronisation between workgroups.  On this
+// part a kernel boundary costs about 2 us, while an agent-scope fence with a
+// last-block merge costs 6-25 us, so the merge is a second kernel.
 //
-// slice_kernel: a row of V logits is cut into G slices; each slice is owned
-// by one 1024-thread workgroup that reads it from HBM exactly once (16-byte
-// loads, all issued up front, held in VGPRs) and reduces it to a summary:
-//   * the penalties for the slice's history tokens (LDS hash, values taken
-//     from the registers that hold the logits -- no second read),
-//   * the slice max m_s (and, for greedy rows, the lowest index attaining it),
-//   * the candidates: every slice element at or above a threshold tau_s that
-//     is provably below the row's kept set --
-//       rule M (min-p active):   tau_s = fl(m_s + ln min_p)  <= the row's cut
-//       rule K (top-k bounds the kept set): tau_s = the slice's k-th largest
-//       rule P (top-p only):     tau_s = the slice's cap/2-th largest,
-//   * bounds on the normaliser Z = sum_i exp_fix44(l_i - m): the exact
-//     fixed-point mass of the elements within 8 nats of m_s (a lower bound,
-//     with the count of the rest for an upper bound), plus a hardware-exp
-//     float estimate when top-p may cut without min-p behind it.
-// Workgroups never wait for each other: no fences, no atomics across them.
+// slice_kernel: row b is cut into G slices.  One 1024-thread workgroup per
+// slice reads its slice from HBM exactly once: 16-byte loads, all issued up
+// front, held in VGPRs.  It reduces the slice to a 64-byte summary plus a
+// short candidate list.  Every VALU op per element costs about a quarter of
+// a microsecond over a full batch, so the per-element work is only the
+// unpack and a max.  The rest is done per 16-byte group or per rare element:
+//   * Penalties.  The history window becomes a dense u16 code per slice
+//     element in LDS: the count in the frequency window, plus flags for the
+//     repetition and presence windows.  The thread holding a group reads that
+//     group's codes with one LDS load and recomputes the few penalised
+//     values.  A penalised bf16 value cannot live in the packed register, so
+//     it moves to a short LDS list and its register slot is set to -inf.
+//   * The slice max m_s and the max of every 16-byte group.
+//   * The candidate threshold tau_s.  No kept element of the row can fall
+//     below it:
+//       - min-p: fl(m_s + ln min_p);
+//       - top-k: a threshold with at least k slice elements at or above it,
+//         found by counting group maxima against a ladder of thresholds below
+//         m_s;
+//       - top-p alone: the lowest ladder rung whose count fits the buffer.
+//   * The candidates, all elements >= tau_s.  They are appended from the rare
+//     groups whose max reaches tau_s.
+//   * Two band counts of groups whose max lies 1.5 / 3.5 nats below tau_s.
+//     They give a lower bound on the normaliser's mass outside the
+//     candidates.
+//   * When the top-p cut needs the normaliser closely, a hardware-exp float
+//     sum over the slice.
 //
-// merge_kernel: one workgroup per row.  Wave 0 merges the G summaries with
-// wave-level primitives (no block barriers): global max, exact fixed-point
-// masses of the candidates, top-k / top-p / min-p in the chain's order, and
-// the inverse-CDF draw over integer weights in vocabulary order -- the same
-// integer contract as the exact engine.  A top-p cut is taken only when it is
-// the same at both ends of the proven [Zlo, Zhi] interval.  A row the
-// candidates cannot settle (capacity overflow, an ambiguous cut, no filter at
-// all) is finished by the whole workgroup with the exact engine.
+// merge_kernel: one workgroup per row.  Wave 0 loads the G summaries and the
+// first 64 candidates of every slice in one round trip.  It keeps up to eight
+// candidates per lane in registers and runs the integer contract over them:
+//   * the proven interval [Zlo, Zhi] for the normaliser;
+//   * top-k / top-p / min-p in the chain's order;
+//   * the inverse-CDF draw.
+// Cut points are found by bitwise searches over value/id composites, with
+// ballot counts and DPP sums.  Larger candidate sets go through LDS with a
+// radix select.  The exact engine finishes a row the candidates cannot
+// settle: a buffer overflow, a top-p cut inside the uncertainty of Z, or no
+// usable bound.  It uses the whole workgroup, and the results are identical,
+// only slower.
 #include "wh_rowops.h"
 
 namespace wh {
 
 constexpr int FT = 1024;          // slice-kernel threads per workgroup
-constexpr int FAST_RMAX = 16;     // max 16-byte loads per thread per slice
-constexpr float ZBAND = 8.0f;     // exact-mass band below the slice max, nats
-
-enum { RULE_GREEDY = 0, RULE_M = 1, RULE_K = 2, RULE_P = 3, RULE_ALL = 4 };
+constexpr int FNW = FT / 64;      // waves per slice workgroup
+constexpr int FAST_NE = 48;       // logits per thread held in VGPRs, at most
+constexpr int GPREF = 4;          // slices per row preferred for small batches
+constexpr int FAST_CAP = 2048;    // candidate capacity per slice
+constexpr int RUNGS = 8;          // thresholds per ladder round
+constexpr int QM = 8;             // merge: candidate slots per lane
+constexpr float BAND1 = 1.5f;     // band floors below tau, nats
+constexpr float BAND2 = 3.5f;
 
 struct SliceHdr {
-  float m;       // slice max (penalised)
-  float tau;     // every slice element >= tau is a candidate
-  int n;         // candidates written (= elements >= tau unless flags)
-  int flags;     // 1: overflow / rule ALL -- the row needs the exact engine
-  float t[3];    // band floors t1 >= t2 >= t3, all <= tau
-  int c[3];      // elements >= t1, >= t2, >= t3 (cumulative, include candidates)
-  int nall;      // elements in the slice
-  int best_i;    // greedy: lowest index attaining the max
-  double zf;     // sum of exp(l - m) over the slice (hardware exp), < 0 if not computed
-  int pad[2];
+  float m;        // slice max (penalised)
+  float tau;      // every slice element >= tau is a candidate
+  int n;          // candidates written
+  int flags;      // 1: candidate overflow or no usable bound -- the row needs the exact engine
+  float t1, t2;   // band floors t1 = tau - 1.5, t2 = tau - 3.5
+  int g1, g2;     // groups (or penalised elements) whose max lies in [t1, tau) / [t2, t1)
+  int nall;       // elements in the slice
+  int best_i;     // greedy rows: lowest index attaining the max
+  double zf;      // sum of exp(l - m) over the slice (hardware exp); < 0 when not computed
+  int pad[4];
 };
 static_assert(sizeof(SliceHdr) == 64, "SliceHdr layout");
 
 struct FastPlan {
-  int G;          // slices per row
-  int SL;         // slice length (multiple of the elements per 16-byte load)
-  int cap;        // candidate capacity per slice
-  int rule_cap;   // largest k (or top-p window) a slice may bound
-  int* path;      // [B] 0: merged from candidates, 1: exact engine (overflow / no filter),
-                  //     2: greedy, 3: exact engine (top-p cut not settled by the bounds)
-  SliceHdr* hdr;  // [B * G]
-  int2* cand;     // [B * G * cap] (value bits, id)
+  int G;           // slices per row
+  int SL;          // slice length (a multiple of the elements per 16-byte load)
+  int cap;         // candidate capacity per slice
+  int rule_cap;    // largest k a slice may bound
+  int pcap;        // capacity of the penalised-element list (bf16 with penalties)
+  int codes_bytes; // LDS bytes of the penalty codes (0 without penalties)
+  int cand_off;    // LDS offset of the candidate buffer
+  int* path;       // [B] 0: merged in registers, 4: merged through LDS, 1: exact engine
+                   //     (overflow / no bound), 2: greedy, 3: exact engine (top-p cut unsettled)
+  SliceHdr* hdr;   // [B * G]
+  int2* cand;      // [B * G * cap] (value bits, id)
 };
-
-__device__ __forceinline__ int choose_rule(int chain, float T, bool use_k, bool use_p, bool use_m, int k, int rule_cap) {
-  if (!(T > 0.0f)) return RULE_GREEDY;
-  if (chain == WH_CHAIN_MLX && use_k && use_p) return k <= rule_cap ? RULE_K : RULE_ALL;
-  if (use_m) return RULE_M;
-  if (use_k) return k <= rule_cap ? RULE_K : RULE_ALL;
-  if (use_p) return RULE_P;
-  return RULE_ALL;
-}
 
 struct RowParams {
   float T, top_p, min_p;
   int top_k;
   bool use_k, use_p, use_m;
-  int rule;
+  bool greedy;
+  bool tk;   // tau from the slice's k-th value
+  bool tm;   // tau from min-p
+  bool tp;   // tau from the candidate capacity (top-p is the only filter that bounds)
+  bool all;  // nothing bounds the kept set: exact engine
 };
 
-__device__ __forceinline__ RowParams row_params(const SampleKArgs& a, int b, int rule_cap) {
+// Both kernels take (SampleKArgs, FastPlan); their kernel-argument segment
+// holds SampleKArgs at offset 0 and FastPlan at the next 8-byte boundary.
+// Reading fields in place (a pointer, not a copy) keeps out-of-line callees
+// and per-row parameter loads from forcing the arguments into private memory.
+struct KernArgs {
+  SampleKArgs a;
+  FastPlan p;
+};
+__device__ __forceinline__ const KernArgs* kernargs() {
+  return (const KernArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+}
+
+// Which bounds the slices may use.  Chain MLX with top-k and top-p computes
+// the top-p mass over the exact top-k set, so there the candidates must hold
+// the whole top-k set and min-p may not raise the threshold.
+// The row's raw parameters: one unconditional load each, from the per-row
+// array or the scalar field (no branch join that waits for the load).
+struct RowRaw {
+  float T, top_p, min_p;
+  int top_k;
+};
+// The loads go through the constant address space: the addresses are
+// uniform and the data is read-only for the kernel's lifetime, so they are
+// scalar loads, counted apart from the vector loads of the logits.
+typedef __attribute__((address_space(4))) const float cfloat;
+typedef __attribute__((address_space(4))) const int cint;
+__device__ __forceinline__ RowRaw row_raw(const SampleKArgs& a, int b) {
+  const SampleKArgs& ka = kernargs()->a;
+  RowRaw r;
+  r.T = *(cfloat*)(a.T_rows ? a.T_rows + b : &ka.T);
+  r.top_p = *(cfloat*)(a.top_p_rows ? a.top_p_rows + b : &ka.top_p);
+  r.min_p = *(cfloat*)(a.min_p_rows ? a.min_p_rows + b : &ka.min_p);
+  r.top_k = *(cint*)(a.top_k_rows ? a.top_k_rows + b : &ka.top_k);
+  return r;
+}
+__device__ __forceinline__ RowParams row_params(const SampleKArgs& a, const RowRaw& raw, int rule_cap) {
   RowParams r;
-  r.T = a.T_rows ? a.T_rows[b] : a.T;
-  r.top_p = a.top_p_rows ? a.top_p_rows[b] : a.top_p;
-  r.min_p = a.min_p_rows ? a.min_p_rows[b] : a.min_p;
-  r.top_k = a.top_k_rows ? a.top_k_rows[b] : a.top_k;
+  r.T = raw.T;
+  r.top_p = raw.top_p;
+  r.min_p = raw.min_p;
+  r.top_k = raw.top_k;
   r.use_k = r.top_k > 0 && r.top_k < a.V;
   r.use_p = r.top_p > 0.0f && r.top_p < 1.0f;
   r.use_m = r.min_p != 0.0f;
-  r.rule = choose_rule(a.chain, r.T, r.use_k, r.use_p, r.use_m, r.top_k, rule_cap);
+  r.greedy = !(r.T > 0.0f);
+  const bool bk = r.use_k && r.top_k <= rule_cap;
+  r.tk = r.tm = r.tp = false;
+  if (!r.greedy) {
+    if (a.chain == WH_CHAIN_MLX && r.use_k && r.use_p) {
+      r.tk = bk;
+    } else {
+      r.tk = bk;
+      r.tm = r.use_m;
+      r.tp = !r.tk && !r.tm && r.use_p;
+    }
+  }
+  r.all = !r.greedy && !r.tk && !r.tm && !r.tp;
   return r;
 }
 
@@ -95,7 +161,7 @@ __device__ __forceinline__ float min_p_log(const SampleKArgs& a, float min_p) {
   return a.min_p_rows ? (float)log((double)min_p) : a.min_p_log;
 }
 
-// Element e of a 16-byte group (DT 0: 4 x float32, DT 1: 8 x bfloat16), -0 -> +0.
+// Element e of a 16-byte group (DT 0: 4 x float32, DT 1: 8 x bfloat16).
 __device__ __forceinline__ uint32_t comp(const uint4& v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
@@ -103,94 +169,175 @@ __device__ __forceinline__ void set_comp(uint4& v, int i, uint32_t x) {
   if (i == 0) v.x = x; else if (i == 1) v.y = x; else if (i == 2) v.z = x; else v.w = x;
 }
 template <int DT>
-__device__ __forceinline__ float grp_elem(const uint4& v, int e) {
-  if (DT == 0) return __uint_as_float(comp(v, e)) + 0.0f;
+__device__ __forceinline__ float elem(const uint4& v, int e) {
+  if (DT == 0) return __uint_as_float(comp(v, e));
   const uint32_t x = comp(v, e >> 1);
-  return __uint_as_float((e & 1) ? (x & 0xFFFF0000u) : (x << 16)) + 0.0f;
+  return __uint_as_float((e & 1) ? (x & 0xFFFF0000u) : (x << 16));
 }
-// Write -inf into slot e of a 16-byte group.
+// The element with -0 mapped to +0 (the value every order and key sees).
 template <int DT>
-__device__ __forceinline__ void grp_kill(uint4& v, int e) {
+__device__ __forceinline__ float elem_n(const uint4& v, int e) {
+  return elem<DT>(v, e) + 0.0f;
+}
+template <int DT>
+__device__ __forceinline__ void kill(uint4& v, int e) {
   if (DT == 0) { set_comp(v, e, 0xFF800000u); return; }
   const uint32_t x = comp(v, e >> 1);
   set_comp(v, e >> 1, (e & 1) ? ((x & 0x0000FFFFu) | 0xFF800000u) : ((x & 0xFFFF0000u) | 0x0000FF80u));
 }
-
-// Dynamic LDS layout of the slice kernel:
-//   [hkeys hcap][hpos/hval hcap][hcnt hcap][bitmap (SL+31)/32] | candidate buffer (cap int2)
-__host__ __device__ __forceinline__ size_t cand_buf_offset(int hcap, int SL) {
-  const size_t o = hcap > 0 ? (size_t)hcap * 12 + (size_t)((SL + 31) / 32) * 4 : 0;
-  return (o + 15) / 16 * 16;
+template <int DT>
+__device__ __forceinline__ float grp_max(const uint4& v) {
+  if (DT == 0)
+    return fmaxf(fmaxf(__uint_as_float(v.x), __uint_as_float(v.y)), fmaxf(__uint_as_float(v.z), __uint_as_float(v.w)));
+  const float a = fmaxf(fmaxf(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u)),
+                        fmaxf(__uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u)));
+  const float c = fmaxf(fmaxf(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u)),
+                        fmaxf(__uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u)));
+  return fmaxf(a, c);
+}
+// u16 penalty code of element e of a group from its codes word(s).
+__device__ __forceinline__ uint32_t code_of(const uint4& cw, int e) {
+  return (comp(cw, e >> 1) >> ((e & 1) * 16)) & 0xFFFFu;
 }
 
-struct SliceSmem {
-  uint64_t hist64[1024];   // slice_kth counters (as 2048 x u32)
-  uint64_t s64[16];
-  double sd[16];
-  float sf[16];
-  int si[16];
-  uint64_t bc64[2];
-  int cnt;
+// Penalty code bits: count in the frequency window (bits 0-12, at most 4096),
+// in the repetition window (bit 13), in the presence window (bit 14).  A flag
+// whose window equals the frequency window is read from the count instead.
+constexpr uint32_t PEN_CNT = 0x1FFFu, PEN_R = 0x2000u, PEN_P = 0x4000u;
+
+struct PenCtx {
+  bool on_r, on_p, on_f, dr, dp;
+  float rep, pres, freq;
+  __device__ __forceinline__ float apply(float v, uint32_t code) const {
+    const int c = (int)(code & PEN_CNT);
+    const bool in_r = dr ? c > 0 : (code & PEN_R) != 0;
+    const bool in_p = dp ? c > 0 : (code & PEN_P) != 0;
+    if (on_r && in_r) v = v < 0.0f ? v * rep : v / rep;
+    if (on_p && in_p) v = v - pres;
+    if (on_f && c > 0) v = v - freq * (float)c;
+    return v + 0.0f;
+  }
 };
 
-// The slice's k-th largest value (k >= 1) over register elements and the
-// penalised hash entries; -inf when the slice holds fewer than k elements.
-// 32-bit keys in three digit passes (11, 11, 10 bits), counts in LDS.
-template <int DT, int R>
-__device__ float slice_kth(const uint4 (&d)[R], int v0, int v1, const int* hk, const float* hv, int hcap,
-                           int k, SliceSmem& sm) {
-  const int tid = threadIdx.x;
-  constexpr int EPT = DT ? 8 : 4;
-  uint32_t* hist = (uint32_t*)sm.hist64;
-  int cnt = 0;
+struct SliceSmem {
+  int cnt;                      // candidates appended
+  int npatch;                   // penalised bf16 elements listed
+  float redm[FNW];
+  int redg[FNW];
+  int lad[3][RUNGS];            // ladder totals per round (zeroed at kernel start)
+  int redb[FNW][2];
+  double redz[FNW];
+};
+
+// Ladder counts: for each rung x_j, the groups whose max is >= x_j plus the
+// listed penalised elements >= x_j, over the whole slice.  Block-wide: wave
+// sums by DPP, then one LDS atomic per wave and rung into round `buf`'s totals.
+template <int R>
+__device__ __forceinline__ void ladder_count(const float (&gm)[R], const int2* patch, int npatch, const float (&x)[RUNGS],
+                                             int (&tot)[RUNGS], int buf, SliceSmem& sm) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  int c[RUNGS];
 #pragma unroll
-  for (int r = 0; r < R; ++r) cnt += (v0 + (r * FT + tid) * EPT < v1) ? EPT : 0;
-  for (int j = tid; j < hcap; j += FT) cnt += hk[j] >= 0 ? 1 : 0;
-  const int total = block_reduce(cnt, sm.si, OpSumI(), 0);
-  if (total < k) return -INFINITY;
-  uint32_t prefix = 0;
-  uint32_t target = (uint32_t)k;
+  for (int j = 0; j < RUNGS; ++j) c[j] = 0;
 #pragma unroll
-  for (int pass = 0; pass < 3; ++pass) {
-    const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
-    const int nb = pass == 2 ? 10 : 11;
-    const uint32_t mask = (1u << nb) - 1u;
-    for (int i = tid; i < 2048; i += FT) hist[i] = 0;
-    __syncthreads();
-    auto add = [&](float l) {
-      const uint32_t key = fkey(l);
-      if (pass > 0 && (key >> (sh + nb)) != prefix) return;
-      atomicAdd(&hist[(key >> sh) & mask], 1u);
-    };
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int g = v0 + (r * FT + tid) * EPT;
-      if (g < v1) {
+    for (int j = 0; j < RUNGS; ++j) c[j] += gm[r] >= x[j] ? 1 : 0;
+  for (int p = tid; p < npatch; p += FT) {
+    const float v = __int_as_float(patch[p].x);
 #pragma unroll
-        for (int e = 0; e < EPT; ++e) add(grp_elem<DT>(d[r], e));
-      }
-    }
-    for (int j = tid; j < hcap; j += FT)
-      if (hk[j] >= 0) add(hv[j]);
-    __syncthreads();
-    const int nbins = 1 << nb;
-    const int hi = nbins - 1 - 2 * tid, lo = hi - 1;
-    const uint64_t h_hi = hi >= 0 ? hist[hi] : 0, h_lo = lo >= 0 ? hist[lo] : 0;
-    uint64_t tot;
-    const uint64_t excl = block_exclusive_scan_u64(h_hi + h_lo, sm.s64, &tot);
-    if (hi >= 0 && excl < target && excl + h_hi >= target) {
-      sm.bc64[0] = (uint64_t)hi;
-      sm.bc64[1] = excl;
-    } else if (lo >= 0 && excl + h_hi < target && excl + h_hi + h_lo >= target) {
-      sm.bc64[0] = (uint64_t)lo;
-      sm.bc64[1] = excl + h_hi;
-    }
-    __syncthreads();
-    prefix = (prefix << nb) | (uint32_t)sm.bc64[0];
-    target -= (uint32_t)sm.bc64[1];
-    __syncthreads();
+    for (int j = 0; j < RUNGS; ++j) c[j] += v >= x[j] ? 1 : 0;
   }
-  return key_to_float(prefix);
+#pragma unroll
+  for (int j = 0; j < RUNGS; ++j) {
+    const int w = wsum_i(c[j]);
+    if (lane == 0 && w) atomicAdd(&sm.lad[buf][j], w);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < RUNGS; ++j) tot[j] = sm.lad[buf][j];
+}
+
+// Candidate threshold from the ladder.
+//   k > 0 (top-k bound): a threshold with at least k slice elements at or
+//     above it -- the highest rung whose group count reaches k (each counted
+//     group holds at least one such element), refined between rungs while the
+//     count exceeds half the buffer; -inf when no rung reaches k.
+//   k <= 0 (top-p alone): the lowest rung whose group count is at most half
+//     the buffer, refined once towards the next rung.
+template <int R>
+__device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* patch, int npatch, float ms, int k, int cap,
+                                            SliceSmem& sm) {
+  // Every rung array is indexed with compile-time indices only (unrolled
+  // loops with selects), so it stays in registers.
+  const float D0[RUNGS] = {0.0f, 0.5f, 1.0f, 2.0f, 4.0f, 8.0f, 16.0f, 32.0f};
+  const int half = cap / 2;
+  float x[RUNGS];
+  int c[RUNGS];
+#pragma unroll
+  for (int j = 0; j < RUNGS; ++j) x[j] = ms - D0[j];
+  ladder_count<R>(gm, patch, npatch, x, c, 0, sm);
+  if (k > 0) {
+    // counts grow with j: hi = last rung with count < k, lo = first with >= k
+    bool found = false;
+    float lo = -INFINITY, hi = INFINITY;
+    int clo = 0;
+#pragma unroll
+    for (int j = 0; j < RUNGS; ++j) {
+      if (!found && c[j] >= k) {
+        found = true;
+        lo = x[j];
+        clo = c[j];
+      }
+      if (!found) hi = x[j];
+    }
+    if (!found) return -INFINITY;
+    for (int round = 1; round < 3 && clo > half && hi != INFINITY; ++round) {
+      const float span = hi - lo;
+#pragma unroll
+      for (int q = 0; q < RUNGS; ++q) x[q] = hi - span * (float)(q + 1) / (float)(RUNGS + 1);
+      ladder_count<R>(gm, patch, npatch, x, c, round, sm);
+      bool f2 = false;
+      float nlo = lo, nhi = hi;
+      int nclo = clo;
+#pragma unroll
+      for (int q = 0; q < RUNGS; ++q) {
+        if (!f2 && c[q] >= k) {
+          f2 = true;
+          nlo = x[q];
+          nclo = c[q];
+        }
+        if (!f2) nhi = x[q];
+      }
+      lo = nlo;
+      hi = nhi;
+      clo = nclo;
+    }
+    return lo;
+  }
+  // counts grow with j: the lowest rung with count <= half, then one refinement
+  // towards the next rung down
+  bool any = false;
+  float sel = ms, nxt = ms;
+#pragma unroll
+  for (int j = 0; j < RUNGS; ++j) {
+    if (c[j] <= half) {
+      any = true;
+      sel = x[j];
+      nxt = j + 1 < RUNGS ? x[j + 1] : x[j];
+    }
+  }
+  if (!any) return ms;
+  if (nxt == sel) return sel;
+  const float span = sel - nxt;
+#pragma unroll
+  for (int q = 0; q < RUNGS; ++q) x[q] = sel - span * (float)(q + 1) / (float)(RUNGS + 1);
+  ladder_count<R>(gm, patch, npatch, x, c, 1, sm);
+  float best = sel;
+#pragma unroll
+  for (int q = 0; q < RUNGS; ++q)
+    if (c[q] <= half) best = x[q];
+  return best;
 }
 
 template <int DT, int R>
@@ -199,80 +346,99 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   __shared__ SliceSmem sm;
   constexpr int EPT = DT ? 8 : 4;
   constexpr int ESZ = DT ? 2 : 4;
-  const int tid = threadIdx.x;
-  const int b = blockIdx.x / P.G, s = blockIdx.x % P.G;
+  constexpr uint32_t NEG = DT ? 0xFF80FF80u : 0xFF800000u;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int b = blockIdx.x / P.G, s = blockIdx.x - b * P.G;
   const int V = a.V;
   const int v0 = s * P.SL, v1 = min(V, v0 + P.SL);
-  const RowParams rp = row_params(a, b, P.rule_cap);
-  SliceHdr* hdr = P.hdr + (long long)b * P.G + s;
-  if (rp.rule == RULE_ALL) {
-    if (tid == 0) hdr->flags = 1;
-    return;
-  }
-  float* out = a.out_rows ? a.out_rows + (long long)b * V : nullptr;
 
-  // 1. the slice, straight into registers
+  // 1. loads, in the order they are needed: the row's parameters (scalar),
+  //    the history window (up to 4 ids per thread) and its length, then the
+  //    slice straight into registers (padding groups read as -inf).  Vector
+  //    loads complete in order, so waiting for the history leaves the logits
+  //    in flight; the compiler barrier keeps every load issued before the
+  //    first wait.
+  const RowRaw raw = row_raw(a, b);
+  const bool pen = a.hcap > 0;
+  constexpr int HPF = 4;
+  const int hs = (int)a.hist_stride;
+  const bool pf = hs <= HPF * FT;
+  int hreg[HPF];
+  int len = 0;
+#pragma unroll
+  for (int q = 0; q < HPF; ++q) hreg[q] = -1;
+  // Every vector load is unconditional, from a clamped in-bounds address, so
+  // the number of loads in flight is the same on every path and each wait is
+  // for exactly the loads it needs.
+  if (pen) {
+    const int32_t* h = a.hist + (long long)b * a.hist_stride;
+#pragma unroll
+    for (int q = 0; q < HPF; ++q) hreg[q] = h[min(tid + q * FT, hs - 1)];
+    len = *(cint*)(a.hist_len + b);
+  }
   const char* rowp = (const char*)a.logits + (size_t)b * a.row_stride * ESZ;
   uint4 d[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int g = v0 + (r * FT + tid) * EPT;
-    d[r] = make_uint4(0u, 0u, 0u, 0u);
-    if (g < v1) d[r] = *(const uint4*)(rowp + (size_t)g * ESZ);
+    d[r] = *(const uint4*)(rowp + (size_t)(g < v1 ? g : v0) * ESZ);
+  }
+  asm volatile("" ::: "memory");
+  const RowParams rp = row_params(a, raw, P.rule_cap);
+  SliceHdr* hdr = P.hdr + (long long)b * P.G + s;
+  if (rp.all) {
+    if (tid == 0) hdr->flags = 1;
+    return;
+  }
+  float* out = a.out_rows ? a.out_rows + (long long)b * V : nullptr;
+  if (tid < 3 * RUNGS) (&sm.lad[0][0])[tid] = 0;
+  if (tid == 0) {
+    sm.cnt = 0;
+    sm.npatch = 0;
   }
 
-  // 2. penalties: history window -> LDS hash of the slice's tokens; the owner
-  //    of each penalised element computes its value from the register copy,
-  //    stores it in the hash and writes -inf into the register slot.  The
-  //    history row (up to 4 ids per thread) and its length are fetched with
-  //    the logits, so their latency overlaps.
-  const int hcap = a.hcap;
-  int32_t* hkeys = (int32_t*)dyn;
-  int32_t* hpos = hkeys + hcap;
-  int32_t* hcnt = hpos + hcap;
-  uint32_t* bm = (uint32_t*)(hcnt + hcap);
-  float* hval = (float*)hpos;
-  if (hcap > 0) {
-    constexpr int HPF = 4;
+  // 2. penalties: dense per-element codes in LDS, applied by the thread that
+  //    holds the element.  The history row (up to 4 ids per thread) and its
+  //    length are fetched together with the logits.
+  uint32_t* codes = (uint32_t*)dyn;
+  int2* patch = (int2*)(dyn + P.codes_bytes);
+  int2* cbuf = (int2*)(dyn + P.cand_off);
+  float pmax = -INFINITY;
+  PenCtx pc;
+  pc.on_r = pc.on_p = pc.on_f = pc.dr = pc.dp = false;
+  pc.rep = a.rep;
+  pc.pres = a.pres;
+  pc.freq = a.freq;
+  if (pen) {
     const int32_t* h = a.hist + (long long)b * a.hist_stride;
-    const int hs = (int)a.hist_stride;
-    const bool pf = hs <= HPF * FT;
-    int hreg[HPF];
-#pragma unroll
-    for (int q = 0; q < HPF; ++q) {
-      const int j = tid + q * FT;
-      hreg[q] = (pf && j < hs) ? h[j] : -1;
-    }
-    int len = a.hist_len ? a.hist_len[b] : 0;
-    const int words = (v1 - v0 + 31) >> 5;
-    for (int t = tid; t < hcap; t += FT) { hkeys[t] = -1; hpos[t] = -1; hcnt[t] = 0; }
-    for (int w = tid; w < words; w += FT) bm[w] = 0u;
+    const int words = P.codes_bytes / 16;
+    for (int w = tid; w < words; w += FT) ((uint4*)codes)[w] = make_uint4(0u, 0u, 0u, 0u);
     len = max(0, min(len, hs));
-    const bool on_r = a.rep != 0.0f, on_p = a.pres != 0.0f, on_f = a.freq != 0.0f;
+    pc.on_r = a.rep != 0.0f;
+    pc.on_p = a.pres != 0.0f;
+    pc.on_f = a.freq != 0.0f;
     auto window = [len](int ctx) { return (ctx <= 0 || ctx > len) ? len : ctx; };
-    const int wr = on_r ? window(a.rep_ctx) : 0;
-    const int wp = on_p ? window(a.pres_ctx) : 0;
-    const int wf = on_f ? window(a.freq_ctx) : 0;
+    const int wr = pc.on_r ? window(a.rep_ctx) : 0;
+    const int wp = pc.on_p ? window(a.pres_ctx) : 0;
+    const int wf = pc.on_f ? window(a.freq_ctx) : 0;
+    pc.dr = pc.on_r && pc.on_f && wr == wf;
+    pc.dp = pc.on_p && pc.on_f && wp == wf;
     const int W = max(wr, max(wp, wf));
-    const int hshift = 32 - a.hlog2, hmask = hcap - 1;
     auto insert = [&](int j, int t) {
       if (t < v0 || t >= v1) return;
-      uint32_t q = ((uint32_t)t * 2654435761u) >> hshift;
-      while (true) {
-        const int old = atomicCAS(&hkeys[q], -1, t);
-        if (old == -1 || old == t) break;
-        q = (q + 1) & hmask;
-      }
-      atomicMax(&hpos[q], j);
-      if (j >= len - wf) atomicAdd(&hcnt[q], 1);
-      atomicOr(&bm[(t - v0) >> 5], 1u << ((t - v0) & 31));
+      const int o = t - v0;
+      const int sh = (o & 1) * 16;
+      const uint32_t add = (pc.on_f && j >= len - wf) ? 1u : 0u;
+      const uint32_t fl = ((pc.on_r && !pc.dr && j >= len - wr) ? PEN_R : 0u) | ((pc.on_p && !pc.dp && j >= len - wp) ? PEN_P : 0u);
+      if (add) atomicAdd(&codes[o >> 1], add << sh);
+      if (fl) atomicOr(&codes[o >> 1], fl << sh);
     };
     __syncthreads();
     if (pf) {
 #pragma unroll
       for (int q = 0; q < HPF; ++q) {
         const int j = tid + q * FT;
-        if (j >= len - W && j < len) insert(j, hreg[q]);
+        if (j >= len - W && j < len) insert(j, hreg[q]);  // len <= hs, so j < hs
       }
     } else {
       for (int j = len - W + tid; j < len; j += FT) insert(j, h[j]);
@@ -282,161 +448,156 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     for (int r = 0; r < R; ++r) {
       const int g = v0 + (r * FT + tid) * EPT;
       if (g < v1) {
-        const int o = g - v0;
-        const uint32_t bits = (bm[o >> 5] >> (o & 31)) & ((1u << EPT) - 1u);
-        if (bits) {
+        const char* cp = (const char*)codes + (size_t)(g - v0) * 2;
+        uint4 cw;
+        if (DT) {
+          cw = *(const uint4*)cp;
+        } else {
+          const uint2 c2 = *(const uint2*)cp;
+          cw = make_uint4(c2.x, c2.y, 0u, 0u);
+        }
+        if ((cw.x | cw.y | cw.z | cw.w) != 0u) {
 #pragma unroll
           for (int e = 0; e < EPT; ++e) {
-            if (!((bits >> e) & 1u)) continue;
-            const int t = g + e;
-            uint32_t q = ((uint32_t)t * 2654435761u) >> hshift;
-            while (hkeys[q] != t) q = (q + 1) & hmask;
-            const int lp = hpos[q], c = hcnt[q];
-            float v = grp_elem<DT>(d[r], e);
-            if (on_r && lp >= len - wr) v = v < 0.0f ? v * a.rep : v / a.rep;
-            if (on_p && lp >= len - wp) v = v - a.pres;
-            if (on_f && c > 0) v = v - a.freq * (float)c;
-            hval[q] = v + 0.0f;
-            grp_kill<DT>(d[r], e);
+            const uint32_t code = code_of(cw, e);
+            if (!code) continue;
+            const float v = pc.apply(elem_n<DT>(d[r], e), code);
+            if (DT) {
+              const int slot = atomicAdd(&sm.npatch, 1);
+              if (slot < P.pcap) patch[slot] = make_int2(__float_as_int(v), g + e);
+              kill<DT>(d[r], e);
+              pmax = fmaxf(pmax, v);
+            } else {
+              set_comp(d[r], e, __float_as_uint(v));
+            }
           }
         }
       }
     }
-    __syncthreads();
   }
-  auto each_pen = [&](auto f) {
-    for (int j = tid; j < hcap; j += FT) {
-      const int i = hkeys[j];
-      if (i >= 0) f(i, hval[j]);
-    }
-  };
-  auto killed_bits = [&](int g) -> uint32_t {
-    return hcap > 0 ? (bm[(g - v0) >> 5] >> ((g - v0) & 31)) & ((1u << EPT) - 1u) : 0u;
-  };
 
-  // 3. slice max and, for greedy rows, the lowest index attaining it
-  const bool greedy = rp.rule == RULE_GREEDY;
-  float mx = -INFINITY;
-  int mi = 0x7FFFFFFF;
+  // 3. group maxima and the slice max (one block reduction); padding groups
+  //    (duplicate loads) become -inf here
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (v0 + (r * FT + tid) * EPT >= v1) d[r] = make_uint4(NEG, NEG, NEG, NEG);
+  float gm[R];
+  float mx = pmax;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int g = v0 + (r * FT + tid) * EPT;
-    if (g < v1) {
+    gm[r] = grp_max<DT>(d[r]);
+    mx = fmaxf(mx, gm[r]);
+  }
+  mx = wmax_f(mx);
+  if (lane == 0) sm.redm[wv] = mx;
+  __syncthreads();
+  float ms = sm.redm[0];
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        const float l = grp_elem<DT>(d[r], e);
-        if (greedy) {
-          if (mi == 0x7FFFFFFF || l > mx) { mx = l; mi = g + e; }
-        } else {
-          mx = fmaxf(mx, l);
-        }
+  for (int w = 1; w < FNW; ++w) ms = fmaxf(ms, sm.redm[w]);
+  const int npatch_raw = sm.npatch;
+  const int npatch = min(npatch_raw, P.pcap);
+
+  if (rp.greedy) {
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int g = v0 + (r * FT + tid) * EPT;
+      if (gm[r] == ms && bi == 0x7FFFFFFF) {
+#pragma unroll
+        for (int e = 0; e < EPT; ++e)
+          if (bi == 0x7FFFFFFF && g + e < v1 && elem<DT>(d[r], e) == ms) bi = g + e;
       }
     }
-  }
-  each_pen([&](int i, float l) {
-    if (greedy) {
-      if (mi == 0x7FFFFFFF || l > mx || (l == mx && i < mi)) { mx = l; mi = i; }
-    } else {
-      mx = fmaxf(mx, l);
-    }
-  });
-  const float ms = block_reduce(mx, sm.sf, OpMaxF(), -INFINITY);
-
-  if (greedy) {
-    const int cand = (mi != 0x7FFFFFFF && mx == ms) ? mi : 0x7FFFFFFF;
-    const int bi = block_reduce(cand, sm.si, OpMinI(), 0x7FFFFFFF);
+    for (int p = tid; p < npatch; p += FT)
+      if (__int_as_float(patch[p].x) == ms) bi = min(bi, patch[p].y);
+    bi = wmin_i(bi);
+    if (lane == 0) sm.redg[wv] = bi;
     if (out) {  // Whallm's sampling_logprobs returns the (penalised) logits at T == 0
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int g = v0 + (r * FT + tid) * EPT;
         if (g < v1) {
 #pragma unroll
-          for (int e = 0; e < EPT; ++e) out[g + e] = grp_elem<DT>(d[r], e);
+          for (int e = 0; e < EPT; ++e) out[g + e] = elem_n<DT>(d[r], e);
         }
       }
-      __syncthreads();
-      each_pen([&](int i, float l) { out[i] = l; });
     }
+    __syncthreads();
+    if (out)
+      for (int p = tid; p < npatch; p += FT) out[patch[p].y] = __int_as_float(patch[p].x);
     if (tid == 0) {
+      int best = sm.redg[0];
+      for (int w = 1; w < FNW; ++w) best = min(best, sm.redg[w]);
       hdr->m = ms;
-      hdr->best_i = bi;
-      hdr->flags = 0;
+      hdr->best_i = best;
+      hdr->flags = npatch_raw > P.pcap ? 1 : 0;
       hdr->n = 0;
     }
     return;
   }
 
-  // 4. candidate threshold and the band thresholds below it
-  float tau;
-  if (rp.rule == RULE_M) tau = ms + min_p_log(a, rp.min_p);
-  else tau = slice_kth<DT, R>(d, v0, v1, hkeys, hval, hcap, rp.rule == RULE_K ? rp.top_k : P.rule_cap, sm);
-  const float t1 = fminf(tau, ms - 4.5f), t2 = fminf(t1, ms - 6.0f), t3 = fminf(t2, ms - 8.0f);
-  const bool need_zf = rp.use_p && !rp.use_m;
+  // 4. candidate threshold
+  float tau = -INFINITY;
+  if (rp.tm) tau = ms + min_p_log(a, rp.min_p);
+  if (rp.tk || rp.tp) {
+    const float tl = ladder_tau<R>(gm, patch, npatch, ms, rp.tk ? rp.top_k : 0, P.cap, sm);
+    tau = rp.tm ? fmaxf(tau, tl) : tl;
+  }
+  const float t1 = tau - BAND1, t2 = tau - BAND2;
+  const bool need_zf = rp.use_p && !rp.tm;
 
-  // 5. one pass: candidates (wave-aggregated appends to LDS), band counts
-  //    (wave ballots), optional hardware-exp estimate of sum exp(l - ms)
-  int2* buf = (int2*)(dyn + cand_buf_offset(hcap, P.SL));
-  if (tid == 0) sm.cnt = 0;
-  __syncthreads();
-  const int lane = tid & 63;
-  int c1 = 0, c2 = 0, c3 = 0, nall = 0;  // c*: wave-uniform ballot counts
+  // 5. candidates from the groups whose max reaches tau; group band counts;
+  //    optional hardware-exp sum
+  int n1 = 0, n2 = 0;
   float zs = 0.0f;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int g = v0 + (r * FT + tid) * EPT;
-    const bool in = g < v1;
-    const uint32_t killed = in ? killed_bits(g) : 0xFFu;
+    const float x = gm[r];
+    n1 += (x >= t1 && !(x >= tau)) ? 1 : 0;
+    n2 += (x >= t2 && !(x >= t1)) ? 1 : 0;
+    if (x >= tau) {
+      const int g = v0 + (r * FT + tid) * EPT;
+      uint4 cw = make_uint4(0u, 0u, 0u, 0u);
+      if (DT && pen && g < v1) cw = *(const uint4*)((const char*)codes + (size_t)(g - v0) * 2);
 #pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const float l = grp_elem<DT>(d[r], e);
-      const bool valid = in && !((killed >> e) & 1u);
-      nall += valid ? 1 : 0;
-      const uint64_t mk = __ballot(valid && l >= tau);
-      if (mk) {
-        int base = 0;
-        if (lane == 0) base = atomicAdd(&sm.cnt, (int)__popcll(mk));
-        base = __shfl(base, 0, 64);
-        if (valid && l >= tau) {
-          const int slot = base + (int)__popcll(mk & ((1ull << lane) - 1ull));
-          if (slot < P.cap) buf[slot] = make_int2(__float_as_int(l), g + e);
+      for (int e = 0; e < EPT; ++e) {
+        const float l = elem_n<DT>(d[r], e);
+        if (l >= tau && g + e < v1 && !(DT && code_of(cw, e))) {
+          const int slot = atomicAdd(&sm.cnt, 1);
+          if (slot < P.cap) cbuf[slot] = make_int2(__float_as_int(l), g + e);
         }
       }
-      c1 += (int)__popcll(__ballot(valid && l >= t1));
-      c2 += (int)__popcll(__ballot(valid && l >= t2));
-      c3 += (int)__popcll(__ballot(valid && l >= t3));
-      if (need_zf && valid) zs += __expf(l - ms);
+    }
+    if (need_zf) {
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) zs += __expf(elem<DT>(d[r], e) - ms);
     }
   }
-  int p1 = 0, p2 = 0, p3 = 0;
-  each_pen([&](int i, float l) {
-    ++nall;
-    if (l >= tau) {
+  for (int p = tid; p < npatch; p += FT) {
+    const float v = __int_as_float(patch[p].x);
+    n1 += (v >= t1 && !(v >= tau)) ? 1 : 0;
+    n2 += (v >= t2 && !(v >= t1)) ? 1 : 0;
+    if (v >= tau) {
       const int slot = atomicAdd(&sm.cnt, 1);
-      if (slot < P.cap) buf[slot] = make_int2(__float_as_int(l), i);
+      if (slot < P.cap) cbuf[slot] = make_int2(patch[p].x, patch[p].y);
     }
-    p1 += l >= t1;
-    p2 += l >= t2;
-    p3 += l >= t3;
-    if (need_zf) zs += __expf(l - ms);
-  });
-  // one combined block reduction
-  const int wv = tid >> 6;
-  int q1 = wave_sum_i(p1) + c1, q2 = wave_sum_i(p2) + c2, q3 = wave_sum_i(p3) + c3, qa = wave_sum_i(nall);
-  const double qz = need_zf ? wave_sum_f64((double)zs) : 0.0;
+    if (need_zf) zs += __expf(v - ms);
+  }
+  n1 = wsum_i(n1);
+  n2 = wsum_i(n2);
+  const double zw = need_zf ? wsum_f64((double)zs) : 0.0;
   if (lane == 0) {
-    sm.si[wv] = q1;
-    ((int*)sm.s64)[wv] = q2;
-    ((int*)sm.s64)[16 + wv] = q3;
-    sm.sf[wv] = __int_as_float(qa);
-    sm.sd[wv] = qz;
+    sm.redb[wv][0] = n1;
+    sm.redb[wv][1] = n2;
+    sm.redz[wv] = zw;
   }
   __syncthreads();
   const int n = sm.cnt;
   const int nw = min(n, P.cap);
   int2* gc = P.cand + ((long long)b * P.G + s) * P.cap;
-  for (int j = tid; j < nw; j += FT) gc[j] = buf[j];
+  for (int j = tid; j < nw; j += FT) gc[j] = cbuf[j];
   if (out) {
-    // non-candidates are never kept; the merge overwrites the kept ones
+    // non-candidates are never kept; the merge writes the kept ones
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int g = v0 + (r * FT + tid) * EPT;
@@ -447,39 +608,239 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     }
   }
   if (tid == 0) {
-    int s1 = 0, s2 = 0, s3 = 0, sa = 0;
+    int s1 = 0, s2 = 0;
     double sz = 0.0;
-    const int nwv = FT / 64;
-    for (int w = 0; w < nwv; ++w) {
-      s1 += sm.si[w];
-      s2 += ((int*)sm.s64)[w];
-      s3 += ((int*)sm.s64)[16 + w];
-      sa += __float_as_int(sm.sf[w]);
-      sz += sm.sd[w];
+    for (int w = 0; w < FNW; ++w) {
+      s1 += sm.redb[w][0];
+      s2 += sm.redb[w][1];
+      sz += sm.redz[w];
     }
     hdr->m = ms;
     hdr->tau = tau;
     hdr->n = nw;
-    hdr->flags = n > P.cap ? 1 : 0;
-    hdr->t[0] = t1;
-    hdr->t[1] = t2;
-    hdr->t[2] = t3;
-    hdr->c[0] = s1;
-    hdr->c[1] = s2;
-    hdr->c[2] = s3;
-    hdr->nall = sa;
+    hdr->flags = (n > P.cap || npatch_raw > P.pcap) ? 1 : 0;
+    hdr->t1 = t1;
+    hdr->t2 = t2;
+    hdr->g1 = s1;
+    hdr->g2 = s2;
+    hdr->nall = v1 - v0;
+    hdr->best_i = 0;
     hdr->zf = need_zf ? sz : -1.0;
   }
 }
 
 // ---------------------------------------------------------------------------
-// Wave-level merge.
+// Merge.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
   __builtin_amdgcn_wave_barrier();
 }
 
+struct ZBounds {
+  uint64_t lo, hi;
+};
+
+// [Zlo, Zhi] for Z = sum_i exp_fix44(l_i - m) over the row, from the slice
+// summaries (lane s < G holds slice s) and the exact candidate mass Scand.
+//  * Lower bound: the candidates' exact masses, plus for every group counted
+//    in a band [t_j, t_(j-1)) at least one element of mass
+//    >= floor(2^44 e^(t_j - m) (1 - eps)) - 1.
+//  * Upper bound: every non-candidate is below tau.
+//  * When every slice carries its float sum zf (hardware exp, relative error
+//    far below eps = 2e-4 for every term that exp_fix44 does not flush to 0),
+//    both bounds are also taken from zf.
+__device__ __forceinline__ ZBounds z_bounds(const SliceHdr& hd, bool own, float m, uint64_t Scand) {
+  const double SC = 17592186044416.0, EPS = 2e-4;
+  double lo = 0.0, hi = 0.0, zl = 0.0, zh = 0.0;
+  int no_zf = 0;
+  if (own && hd.m != -INFINITY) {
+    auto wlo = [&](float t) {
+      return t == -INFINITY ? 0.0 : fmax(floor(exp((double)t - (double)m) * SC * (1.0 - EPS)) - 1.0, 0.0);
+    };
+    lo = (double)hd.g1 * wlo(hd.t1) + (double)hd.g2 * wlo(hd.t2);
+    hi = (double)(hd.nall - hd.n) * (exp((double)hd.tau - (double)m) * SC * (1.0 + EPS) + 1.0);
+    if (hd.zf >= 0.0) {
+      const double sc = exp((double)hd.m - (double)m) * SC;
+      zl = hd.zf * sc * (1.0 - EPS) - (double)hd.nall;
+      zh = hd.zf * sc * (1.0 + EPS) + (double)hd.nall;
+    } else {
+      no_zf = 1;
+    }
+  }
+  lo = wsum_f64(lo);
+  hi = wsum_f64(hi);
+  zl = wsum_f64(zl);
+  zh = wsum_f64(zh);
+  const bool allzf = wsum_i(no_zf) == 0;
+  const double LIM = 4.0e18;
+  ZBounds z;
+  z.lo = Scand + (uint64_t)fmax(lo, 0.0);
+  z.hi = (hi >= LIM) ? (1ull << 62) : Scand + (uint64_t)ceil(hi);
+  if (allzf) {
+    const uint64_t a = zl <= 0.0 ? 0ull : (uint64_t)zl;
+    const uint64_t c = zh >= LIM ? (1ull << 62) : (uint64_t)ceil(zh);
+    z.lo = a > z.lo ? a : z.lo;
+    z.hi = c < z.hi ? c : z.hi;
+  }
+  if (z.hi > (1ull << 62)) z.hi = 1ull << 62;
+  return z;
+}
+
+// Bits common to lo and hi above their highest differing bit (lower bits
+// cleared), and the number of bits below that point.  Written with shifts by
+// constants only.
+__device__ __forceinline__ uint32_t common_prefix(uint32_t lo, uint32_t hi, int& nbits) {
+  uint32_t d = lo ^ hi;
+  d |= d >> 1;
+  d |= d >> 2;
+  d |= d >> 4;
+  d |= d >> 8;
+  d |= d >> 16;
+  nbits = __popc(d);
+  return lo & ~d;
+}
+
+// Candidates in registers: QM slots per lane, alive bits in `al`.
+struct RegStore {
+  float cl[QM];
+  int ci[QM];
+  uint64_t w[QM];  // exp_fix44(l - m) (replaced by the draw weights at the end)
+  uint32_t al;
+
+  __device__ __forceinline__ bool on(int t) const { return (al >> t) & 1u; }
+  template <typename F>
+  __device__ __forceinline__ int count_if(F f) const {
+    int c = 0;
+#pragma unroll
+    for (int t = 0; t < QM; ++t) c += ballot_count(on(t) && f(t));
+    return c;
+  }
+  template <typename F>
+  __device__ __forceinline__ uint64_t mass_if(F f) const {
+    uint64_t z = 0;
+#pragma unroll
+    for (int t = 0; t < QM; ++t) z += (on(t) && f(t)) ? w[t] : 0ull;
+    return wsum_u64(z);
+  }
+  template <typename F>
+  __device__ __forceinline__ void keep_if(F f) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int t = 0; t < QM; ++t) m |= (on(t) && f(t)) ? (1u << t) : 0u;
+    al = m;
+  }
+  // Smallest / largest key and id over alive slots where f holds (wave).
+  template <typename F>
+  __device__ __forceinline__ void key_range(F f, uint32_t& kmn, uint32_t& kmx) const {
+    kmn = 0xFFFFFFFFu;
+    kmx = 0u;
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      const uint32_t k = fkey(cl[t]);
+      const bool p = on(t) && f(t);
+      kmn = p && k < kmn ? k : kmn;
+      kmx = p && k > kmx ? k : kmx;
+    }
+    kmn = wmin_u32(kmn);
+    kmx = wmax_u32(kmx);
+  }
+  template <typename F>
+  __device__ __forceinline__ void id_range(F f, uint32_t& imn, uint32_t& imx) const {
+    imn = 0xFFFFFFFFu;
+    imx = 0u;
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      const uint32_t i = (uint32_t)ci[t];
+      const bool p = on(t) && f(t);
+      imn = p && i < imn ? i : imn;
+      imx = p && i > imx ? i : imx;
+    }
+    imn = wmin_u32(imn);
+    imx = wmax_u32(imx);
+  }
+
+  __device__ __forceinline__ int count() const { return count_if([](int) { return true; }); }
+  __device__ __forceinline__ uint64_t mass(bool cov_only, float tcov) const {
+    return mass_if([&](int t) { return !cov_only || cl[t] >= tcov; });
+  }
+  __device__ __forceinline__ void none() { al = 0; }
+  __device__ __forceinline__ void keep_min(float thr) {
+    keep_if([&](int t) { return cl[t] >= thr; });
+  }
+  // Top-k in order A (value desc, id asc) over the alive slots.
+  __device__ __forceinline__ void keep_topk(int k) {
+    if (count() <= k) return;
+    uint32_t kmn, kmx;
+    key_range([](int) { return true; }, kmn, kmx);
+    int nb;
+    uint32_t x = common_prefix(kmn, kmx, nb);
+    // largest x with #(key >= x) >= k: the k-th largest key
+    for (int bit = nb - 1; bit >= 0; --bit) {
+      const uint32_t tr = x | (1u << bit);
+      if (count_if([&](int t) { return fkey(cl[t]) >= tr; }) >= k) x = tr;
+    }
+    const uint32_t v = x;
+    const int need = k - count_if([&](int t) { return fkey(cl[t]) > v; });
+    const int ce = count_if([&](int t) { return fkey(cl[t]) == v; });
+    if (ce <= need) {
+      keep_if([&](int t) { return fkey(cl[t]) >= v; });
+      return;
+    }
+    // ties at v: keep the `need` lowest ids
+    uint32_t imn, imx;
+    id_range([&](int t) { return fkey(cl[t]) == v; }, imn, imx);
+    int ni;
+    uint32_t z = common_prefix(imn, imx, ni);
+    for (int bit = ni - 1; bit >= 0; --bit) {
+      const uint32_t tr = z | (1u << bit);
+      if (count_if([&](int t) { return fkey(cl[t]) == v && (uint32_t)ci[t] < tr; }) < need) z = tr;
+    }
+    keep_if([&](int t) {
+      const uint32_t k2 = fkey(cl[t]);
+      return k2 > v || (k2 == v && (uint32_t)ci[t] <= z);
+    });
+  }
+  // The element (order P: value desc, id desc) at which the cumulative mass
+  // over alive covered slots first reaches R (0 < R <= that mass).
+  __device__ __forceinline__ void p_cut(uint64_t R, float tcov, uint32_t& vk, uint32_t& vid) const {
+    auto cov = [&](int t) { return cl[t] >= tcov; };
+    uint32_t kmn, kmx;
+    key_range(cov, kmn, kmx);
+    int nb;
+    uint32_t x = common_prefix(kmn, kmx, nb);
+    for (int bit = nb - 1; bit >= 0; --bit) {
+      const uint32_t tr = x | (1u << bit);
+      if (mass_if([&](int t) { return cov(t) && fkey(cl[t]) >= tr; }) >= R) x = tr;
+    }
+    const uint32_t v = x;
+    const uint64_t need = R - mass_if([&](int t) { return cov(t) && fkey(cl[t]) > v; });
+    uint32_t imn, imx;
+    id_range([&](int t) { return cov(t) && fkey(cl[t]) == v; }, imn, imx);
+    int ni;
+    uint32_t y = common_prefix(imn, imx, ni);
+    // largest y with mass(ties with id >= y) >= need
+    for (int bit = ni - 1; bit >= 0; --bit) {
+      const uint32_t tr = y | (1u << bit);
+      if (mass_if([&](int t) { return cov(t) && fkey(cl[t]) == v && (uint32_t)ci[t] >= tr; }) >= need) y = tr;
+    }
+    vk = v;
+    vid = y;
+  }
+  __device__ __forceinline__ bool keep_pcut(uint64_t Rlo, uint64_t Rhi, float tcov) {
+    uint32_t k0, i0, k1, i1;
+    p_cut(Rlo, tcov, k0, i0);
+    p_cut(Rhi, tcov, k1, i1);
+    if (k0 != k1 || i0 != i1) return false;
+    keep_if([&](int t) {
+      const uint32_t k = fkey(cl[t]);
+      return k > k0 || (k == k0 && (uint32_t)ci[t] >= i0);
+    });
+    return true;
+  }
+};
+
+// Candidates in LDS (any number), walked by wave 0.
 struct MergeSmem {
   uint64_t hist[1024];
   uint64_t bc64[2];
@@ -497,14 +858,11 @@ struct WaveCands {
 
 // Wave-level radix select (same contract as radix_select): the composite of
 // the element at which the cumulative measure over kept candidates first
-// reaches target (0 < target <= total).
+// reaches target (0 < target <= total).  Digits start below the bits common
+// to every kept composite.
 template <int ORD, typename Meas>
 __device__ uint64_t wave_radix_select(const WaveCands& src, const Pred& pr, Meas meas, uint64_t target, MergeSmem& sm) {
   const int lane = threadIdx.x & 63;
-  // Bits above the highest bit in which two kept composites differ are
-  // common to all of them: start the 10-bit digits below it, so the first
-  // pass spreads the candidates over the bins instead of piling them into
-  // one (LDS atomics on one address serialise).
   uint64_t cmin = ~0ull, cmax = 0;
   src.each([&](int i, float l) {
     if (!pr.keep(i, l)) return;
@@ -512,15 +870,11 @@ __device__ uint64_t wave_radix_select(const WaveCands& src, const Pred& pr, Meas
     cmin = c < cmin ? c : cmin;
     cmax = c > cmax ? c : cmax;
   });
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t a = __shfl_xor(cmin, o, 64), b = __shfl_xor(cmax, o, 64);
-    cmin = a < cmin ? a : cmin;
-    cmax = b > cmax ? b : cmax;
-  }
-  if (cmax < cmin) return 0;  // nothing kept (callers never ask)
+  cmin = dpp_reduce_u64(cmin, [](uint64_t a, uint64_t b) { return a < b ? a : b; });
+  cmax = dpp_reduce_u64(cmax, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
+  if (cmax < cmin) return 0;
   const uint64_t diff = cmin ^ cmax;
-  const int top = diff ? 64 - __clzll((long long)diff) : 1;  // bits that vary
+  const int top = diff ? 64 - __clzll((long long)diff) : 1;
   const int PASSES = (top + 9) / 10;
   uint64_t prefix = cmax >> (10 * PASSES);
   for (int pass = 0; pass < PASSES; ++pass) {
@@ -564,256 +918,339 @@ __device__ uint64_t wave_radix_select(const WaveCands& src, const Pred& pr, Meas
   return prefix;
 }
 
+struct LdsStore {
+  WaveCands src;
+  Pred pr;
+  float m;
+  MergeSmem* sm;
+
+  __device__ __forceinline__ int count() const {
+    int c = 0;
+    src.each([&](int i, float l) { c += pr.keep(i, l) ? 1 : 0; });
+    return wsum_i(c);
+  }
+  __device__ __forceinline__ uint64_t mass(bool cov_only, float tcov) const {
+    Pred p = pr;
+    if (cov_only) p.cov = tcov;
+    uint64_t z = 0;
+    const float mm = m;
+    src.each([&](int i, float l) { if (p.keep(i, l)) z += exp_fix44(l - mm); });
+    return wsum_u64(z);
+  }
+  __device__ __forceinline__ void none() { pr.none = 1; }
+  __device__ __forceinline__ void keep_min(float thr) {
+    pr.use_m = 1;
+    pr.thr = thr;
+  }
+  __device__ __forceinline__ void keep_topk(int k) {
+    if (count() <= k) return;
+    const uint64_t ck = wave_radix_select<ORD_A>(src, pr, [](int, float) { return (uint64_t)1; }, (uint64_t)k, *sm);
+    pr.use_k = 1;
+    pr.ck = ck;
+  }
+  __device__ __forceinline__ bool keep_pcut(uint64_t Rlo, uint64_t Rhi, float tcov) {
+    Pred pc = pr;
+    pc.cov = tcov;
+    const float mm = m;
+    auto mass_fn = [mm](int, float l) { return exp_fix44(l - mm); };
+    const uint64_t clo = wave_radix_select<ORD_P>(src, pc, mass_fn, Rlo, *sm);
+    const uint64_t chi = wave_radix_select<ORD_P>(src, pc, mass_fn, Rhi, *sm);
+    if (clo != chi) return false;
+    pr.use_p = 1;
+    pr.cp = clo;
+    return true;
+  }
+};
+
+// The filters in the chain's order over a candidate store.  Returns false when
+// the top-p cut is not settled by [Zlo, Zhi] (the row goes to the exact engine).
+template <typename St>
+__device__ __forceinline__ bool run_filters(St& st, const SampleKArgs& a, const RowParams& rp, float m, float tcov, ZBounds zb) {
+  const float theta = (float)(1.0 - (double)rp.top_p);
+  bool none = false;
+  // Top-p keeps i iff S - head_excl(i) > floor(theta Z).  With Z only known
+  // to lie in [Zlo, Zhi] the cut is taken when both ends agree.  S is the
+  // alive mass: exact when s_exact (after an exact top-k), else Z itself.
+  auto apply_p = [&](bool s_exact) -> bool {
+    if (zb.lo > zb.hi) return false;
+    long long Rlo, Rhi;
+    if (s_exact) {
+      const long long S = (long long)st.mass(false, tcov);
+      Rlo = S - (long long)floor_theta_z(theta, zb.hi);
+      Rhi = S - (long long)floor_theta_z(theta, zb.lo);
+    } else {
+      Rlo = (long long)(zb.lo - floor_theta_z(theta, zb.lo));
+      Rhi = (long long)(zb.hi - floor_theta_z(theta, zb.hi));
+    }
+    if (Rhi <= 0) {
+      st.none();
+      none = true;
+      return true;
+    }
+    if (Rlo <= 0) return false;
+    // Candidates at or above tcov (the largest slice threshold) have every
+    // element ranked above them among the candidates.
+    const long long Scov = (long long)st.mass(true, tcov);
+    if (Rlo > Scov) {
+      // every covered element survives; the kept set stays inside the
+      // covered region only when a later filter or the top-k set confines it
+      return !rp.tp;
+    }
+    if (Rhi > Scov) return false;
+    return st.keep_pcut((uint64_t)Rlo, (uint64_t)Rhi, tcov);
+  };
+  const float thr = m + min_p_log(a, rp.min_p);
+  if (a.chain == WH_CHAIN_MLX && rp.use_k && rp.use_p) {
+    // k -> p -> min-p; the candidates hold the whole top-k set
+    st.keep_topk(rp.top_k);
+    if (!apply_p(true)) return false;
+    if (!none && rp.use_m) st.keep_min(thr);
+  } else {
+    // p -> min-p -> k (Whallm), or mlx_lm without top-p and top-k together:
+    // k -> min-p keeps the first k of the min-p set, which is a value prefix
+    if (rp.use_p && !apply_p(false)) return false;
+    if (!none && rp.use_m) st.keep_min(thr);
+    if (!none && rp.use_k && st.count() > rp.top_k) st.keep_topk(rp.top_k);
+  }
+  return true;
+}
+
+// Register merge of row b by wave 0.  `st` holds slots t < G (the first 64
+// candidates of slice t, loaded with the summaries); slots G..G*TS-1 are
+// loaded here.  Returns the path code (0 done, 3 exact engine).
+__device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& P, int b, const RowParams& rp,
+                                          const SliceHdr& hd, int G, float m, float tcov, float ub, RegStore& st, int TS) {
+  const int lane = threadIdx.x & 63;
+  const int hn = lane < G ? hd.n : 0;
+  if (TS > 1) {
+    // second round trip: chunks 1.. of every slice (offsets < 8 * 64 <= cap)
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      if (t >= G) {
+        const int2 c = P.cand[((long long)b * G + t % G) * P.cap + (t / G) * 64 + lane];
+        st.cl[t] = __int_as_float(c.x);
+        st.ci[t] = c.y;
+      }
+    }
+  }
+  st.al = 0;
+#pragma unroll
+  for (int t = 0; t < QM; ++t) {
+    bool valid = false;
+    if (t < G * TS) {
+      const int ns = (int)lane_u32((uint32_t)hn, t % G);
+      valid = (t / G) * 64 + lane < ns;
+    }
+    st.cl[t] = valid ? st.cl[t] : -INFINITY;
+    st.ci[t] = valid ? st.ci[t] : -1;
+    st.al |= valid ? (1u << t) : 0u;
+  }
+#pragma unroll
+  for (int t = 0; t < QM; ++t) st.w[t] = st.on(t) ? exp_fix44(st.cl[t] - m) : 0ull;
+  const uint64_t Scand = st.mass(false, 0.0f);
+  const ZBounds zb = z_bounds(hd, lane < G, m, Scand);
+  if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
+
+  // Draw: integer inverse CDF in vocabulary order over the kept slots.
+  const float invT = (float)(1.0 / (double)rp.T);
+  const float Tc = (float)fmax((double)rp.T, 1e-5);
+  if (rp.T != 1.0f) {
+#pragma unroll
+    for (int t = 0; t < QM; ++t) st.w[t] = st.on(t) ? exp_fix44(chain_scale(a.chain, st.cl[t] - m, invT, Tc)) : 0ull;
+  }
+  const uint64_t ZV = st.mass(false, 0.0f);
+  const int nkept = st.count();
+  if (a.tokens) {
+    int tok = 0;
+    if (ZV) {
+      const uint64_t tgt = draw_target(ub, ZV);
+      uint32_t imn, imx;
+      st.id_range([](int) { return true; }, imn, imx);
+      int ni;
+      uint32_t x = common_prefix(imn, imx, ni);
+      // largest x with sum_{kept, id < x} w <= tgt: the drawn id
+      for (int bit = ni - 1; bit >= 0; --bit) {
+        const uint32_t tr = x | (1u << bit);
+        if (st.mass_if([&](int t) { return (uint32_t)st.ci[t] < tr; }) <= tgt) x = tr;
+      }
+      tok = (int)x;
+    }
+    if (lane == 0) a.tokens[b] = tok;
+  }
+  if (lane == 0 && a.kept) a.kept[b] = nkept;
+  float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
+  if (out) {
+    const double lz = log(ldexp((double)ZV, -44));
+#pragma unroll
+    for (int t = 0; t < QM; ++t)
+      if (st.on(t))
+        out[st.ci[t]] = a.out_mode == WH_OUT_MASKED ? st.cl[t]
+                                                    : (float)((double)chain_scale(a.chain, st.cl[t] - m, invT, Tc) - lz);
+  }
+  return 0;
+}
+
+// LDS merge of row b by wave 0 (any number of candidates).  Returns the path
+// code (4 done, 3 exact engine).
+// The arguments are read in place from the kernel-argument segment (a
+// pointer, not a copy), so calling this out-of-line path forces nothing of
+// the caller's into private memory.
+__device__ __noinline__ int merge_lds(const SampleKArgs* ap, const FastPlan* pp, int b, RowParams rp, int G, float m,
+                                      float tcov, float ub, char* dyn, MergeSmem* smp) {
+  const SampleKArgs& a = *ap;
+  const FastPlan& P = *pp;
+  MergeSmem& sm = *smp;
+  const int lane = threadIdx.x & 63;
+  SliceHdr hd;
+  if (lane < G) hd = P.hdr[(long long)b * G + lane];
+  const int hn = lane < G ? hd.n : 0;
+  float* cv = (float*)dyn;
+  int* ci = (int*)(dyn + (size_t)G * P.cap * sizeof(float));
+  int off = hn;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(off, o, 64);
+    if (lane >= o) off += y;
+  }
+  const int N = __shfl(off, 63, 64);
+  off -= hn;
+  for (int s = 0; s < G; ++s) {
+    const int ns = __shfl(hn, s, 64), os = __shfl(off, s, 64);
+    const int2* src = P.cand + ((long long)b * G + s) * P.cap;
+    for (int j = lane; j < ns; j += 64) {
+      const int2 c = src[j];
+      cv[os + j] = __int_as_float(c.x);
+      ci[os + j] = c.y;
+    }
+  }
+  wave_sync();
+  LdsStore st;
+  st.src = WaveCands{cv, ci, N};
+  st.pr = Pred{0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
+  st.m = m;
+  st.sm = &sm;
+  const uint64_t Scand = st.mass(false, 0.0f);
+  const ZBounds zb = z_bounds(hd, lane < G, m, Scand);
+  if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
+  const float invT = (float)(1.0 / (double)rp.T);
+  const float Tc = (float)fmax((double)rp.T, 1e-5);
+  const Pred pr = st.pr;
+  const WaveCands src = st.src;
+  auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, Tc)); };
+  uint64_t zv = 0;
+  int nk = 0;
+  src.each([&](int i, float l) {
+    if (pr.keep(i, l)) { zv += vw(i, l); ++nk; }
+  });
+  const uint64_t ZV = wsum_u64(zv);
+  const int nkept = wsum_i(nk);
+  if (a.tokens) {
+    int tok = 0;
+    if (ZV) {
+      const uint64_t tgt = draw_target(ub, ZV);
+      tok = 0x3FFFF - (int)wave_radix_select<ORD_ID>(src, pr, vw, tgt + 1, sm);
+    }
+    if (lane == 0) a.tokens[b] = tok;
+  }
+  if (lane == 0 && a.kept) a.kept[b] = nkept;
+  float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
+  if (out) {
+    const double lz = log(ldexp((double)ZV, -44));
+    src.each([&](int i, float l) {
+      if (!pr.keep(i, l)) return;
+      out[i] = a.out_mode == WH_OUT_MASKED ? l : (float)((double)chain_scale(a.chain, l - m, invT, Tc) - lz);
+    });
+  }
+  return 4;
+}
+
+
 __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ ExactSmem esm;
   __shared__ MergeSmem sm;
-  __shared__ int s_fallback;
-  constexpr int SPEC = 64;  // candidates per slice fetched together with the headers
+  __shared__ int s_path;
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int G = P.G;
-  const RowParams rp = row_params(a, b, P.rule_cap);
+  const RowRaw raw = row_raw(a, b);
+  const RowParams rp = row_params(a, raw, P.rule_cap);
   if (tid < 64) {
     const int lane = tid;
-    const SliceHdr* H = P.hdr + (long long)b * G;
-    // one round trip: headers (lane s < G), the row's uniform, and the first
-    // SPEC candidates of every slice
-    SliceHdr hd;
-    if (lane < G) hd = H[lane];
-    const float ub = (a.tokens && rp.rule != RULE_GREEDY) ? a.u[b] : 0.0f;
-    float* cv = (float*)dyn;
-    int* ci = (int*)(dyn + (size_t)G * P.cap * sizeof(float));
-    int2 spec[4];
-    const bool spec_ok = G <= 4 && rp.rule != RULE_GREEDY && rp.rule != RULE_ALL;
-    if (spec_ok) {
+    // one round trip: the summaries (lane s < G), the row's uniform and the
+    // first 64 candidates of every slice.  Every load is unconditional from a
+    // clamped, in-bounds address (lanes >= G and slots >= G read a duplicate
+    // that is ignored), so no branch join waits for a load to land.
+    const SliceHdr hd = P.hdr[(long long)b * G + min(lane, G - 1)];
+    const float ub = (a.tokens && !rp.greedy) ? a.u[b] : 0.0f;
+    RegStore st;
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        if (s < G) spec[s] = P.cand[((long long)b * G + s) * P.cap + lane];
+    for (int t = 0; t < QM; ++t) {
+      const int2 c = P.cand[((long long)b * G + min(t, G - 1)) * P.cap + lane];
+      st.cl[t] = __int_as_float(c.x);
+      st.ci[t] = c.y;
     }
-    const float hm = lane < G ? hd.m : -INFINITY;
-    const int hflag = lane < G ? hd.flags : 0;
-    const float m = wave_max(hm);
-    int fallback = (wave_sum_i(hflag) != 0 || rp.rule == RULE_ALL) ? 1 : 0;
-    if (rp.rule == RULE_GREEDY) {
-      const int cand = (lane < G && hm == m) ? hd.best_i : 0x7FFFFFFF;
-      const int bi = wave_min_i(cand);
-      if (lane == 0) {
-        if (a.tokens) a.tokens[b] = bi;
-        if (a.kept) a.kept[b] = 1;
-        P.path[b] = 2;
-      }
-      fallback = 0;
-    } else if (!fallback) {
-      const int hn = lane < G ? hd.n : 0;
-      float tcov = lane < G ? hd.tau : -INFINITY;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) tcov = fmaxf(tcov, __shfl_xor(tcov, o, 64));
-      // candidate offsets (prefix over the first G lanes)
-      int off = hn;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(off, o, 64);
-        if (lane >= o) off += y;
-      }
-      const int N = __shfl(off, 63, 64);
-      off -= hn;
-      for (int s = 0; s < G; ++s) {
-        const int ns = __shfl(hn, s, 64), os = __shfl(off, s, 64);
-        const int2* src = P.cand + ((long long)b * G + s) * P.cap;
-        int j0 = 0;
-        if (spec_ok) {
-          int2 c = spec[0];
-          if (s == 1) c = spec[1];
-          if (s == 2) c = spec[2];
-          if (s == 3) c = spec[3];
-          if (lane < ns) { cv[os + lane] = __int_as_float(c.x); ci[os + lane] = c.y; }
-          j0 = SPEC;
-        }
-        for (int j = j0 + lane; j < ns; j += 64) {
-          const int2 c = src[j];
-          cv[os + j] = __int_as_float(c.x);
-          ci[os + j] = c.y;
-        }
-      }
-      wave_sync();
-      const WaveCands src{cv, ci, N};
-      Pred pr = {0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
-      auto mass = [m](int, float l) { return exp_fix44(l - m); };
-      auto one = [](int, float) { return (uint64_t)1; };
-      auto count = [&](const Pred& p) {
-        int c = 0;
-        src.each([&](int i, float l) { c += p.keep(i, l) ? 1 : 0; });
-        return wave_sum_i(c);
-      };
-      auto msum = [&](const Pred& p) {
-        uint64_t z = 0;
-        src.each([&](int i, float l) { if (p.keep(i, l)) z += exp_fix44(l - m); });
-        return wave_sum_u64(z);
-      };
-      const float theta = (float)(1.0 - (double)rp.top_p);
-      bool ambiguous = false;
-
-      // Top-p with the normaliser Z = sum_i exp_fix44(l_i - m) known to lie in
-      // [Zlo, Zhi].  S is the alive mass: exact when s_exact, else Z itself.
-      auto apply_p = [&](bool s_exact) {
-        // The candidates contribute their exact masses.  An element below the
-        // candidate cut but at or above band floor t_j (counted by the slice)
-        // has exp_fix44(l - m) >= floor(2^44 e^(t_j - m) (1 - eps)) - 1 and
-        // <= 2^44 e^(t_(j-1) - m) (1 + eps) + 1 (t_0 = tau), with eps = 1e-4
-        // well above exp_fix44's relative error (|t| + 2) 2^-23 for the
-        // arguments that matter; below t3 only the upper bound counts.  With
-        // a float estimate zf (hardware exp, error < 1e-5 including float
-        // sums of < 2^7 terms) the upper bound is zf-based instead.
-        const double SC = 17592186044416.0;
-        const uint64_t Scand = msum(Pred{0, 0, 0, 0, 0, 0, 0.0f, -INFINITY});
-        double lo = 0.0, hi = 0.0;
-        if (lane < G && hd.m != -INFINITY) {
-          const double fl[4] = {(double)hd.tau, (double)hd.t[0], (double)hd.t[1], (double)hd.t[2]};
-          const int cum[4] = {hd.n, hd.c[0], hd.c[1], hd.c[2]};
-          for (int j = 1; j < 4; ++j) {
-            const double cnt = (double)(cum[j] - cum[j - 1]);
-            if (cnt <= 0.0) continue;
-            const double wl = floor(exp(fl[j] - (double)m) * SC * (1.0 - 1e-4)) - 1.0;
-            lo += cnt * fmax(wl, 0.0);
-            hi += cnt * (exp(fl[j - 1] - (double)m) * SC * (1.0 + 1e-4) + 1.0);
-          }
-          hi += (double)(hd.nall - hd.c[2]) * (exp(fl[3] - (double)m) * SC * (1.0 + 1e-4) + 1.0);
-          if (hd.zf >= 0.0) hi = -1.0;  // replaced below
-        }
-        lo = wave_sum_f64(lo) + (double)Scand;
-        bool use_zf = wave_sum_i(lane < G && hd.m != -INFINITY && hd.zf >= 0.0 ? 1 : 0) > 0;
-        double zfh = 0.0;
-        if (lane < G && hd.m != -INFINITY && hd.zf >= 0.0)
-          zfh = hd.zf * exp((double)hd.m - (double)m) * (1.0 + 1e-4) * SC + (double)hd.nall + 1e-6 * SC;
-        if (use_zf) hi = wave_sum_f64(zfh);
-        else hi = wave_sum_f64(hi) + (double)Scand;
-        const uint64_t Zlo = (uint64_t)lo;
-        const uint64_t Zhi = hi >= 4.0e18 ? (1ull << 62) : (uint64_t)ceil(hi);
-        long long Rlo, Rhi;
-        if (s_exact) {
-          const long long S = (long long)msum(pr);
-          Rlo = S - (long long)floor_theta_z(theta, Zhi);
-          Rhi = S - (long long)floor_theta_z(theta, Zlo);
-        } else {
-          Rlo = (long long)(Zlo - floor_theta_z(theta, Zlo));
-          Rhi = (long long)(Zhi - floor_theta_z(theta, Zhi));
-        }
-        if (Rhi <= 0) { pr.none = 1; return; }
-        if (Rlo <= 0) { ambiguous = true; return; }
-        Pred pc = pr;
-        pc.cov = tcov;
-        const long long Scov = (long long)msum(pc);
-        if (Rlo > Scov) {
-          // every covered element survives; the kept set stays inside the
-          // covered region only if a later filter confines it there (the
-          // min-p cut is >= every slice threshold; the top-k set is covered)
-          if (rp.rule == RULE_P) ambiguous = true;
-          return;
-        }
-        if (Rhi > Scov) { ambiguous = true; return; }
-        const uint64_t clo = wave_radix_select<ORD_P>(src, pc, mass, (uint64_t)Rlo, sm);
-        const uint64_t chi = wave_radix_select<ORD_P>(src, pc, mass, (uint64_t)Rhi, sm);
-        if (clo != chi) { ambiguous = true; return; }
-        pr.use_p = 1;
-        pr.cp = clo;
-      };
-      auto apply_m = [&]() {
-        pr.use_m = 1;
-        pr.thr = m + min_p_log(a, rp.min_p);
-      };
-      if (a.chain == WH_CHAIN_MLX && rp.rule == RULE_K) {
-        // the candidates hold the whole top-k set (at least k of them)
-        if (rp.use_k) {
-          pr.ck = wave_radix_select<ORD_A>(src, pr, one, (uint64_t)rp.top_k, sm);
-          pr.use_k = 1;
-        }
-        if (rp.use_p) apply_p(rp.use_k);
-        if (!ambiguous && rp.use_m && !pr.none) apply_m();
-      } else if (a.chain == WH_CHAIN_MLX) {
-        // rule M or P: no top-p together with top-k here.  k -> min-p: the
-        // min-p set is a value prefix held by the candidates; with more than k
-        // members the row's first k (order A) are its first k, else top-k
-        // keeps all of it.
-        if (rp.use_p) apply_p(false);
-        if (!ambiguous && rp.use_m && !pr.none) apply_m();
-        if (!ambiguous && rp.use_k && !pr.none && count(pr) > rp.top_k) {
-          pr.ck = wave_radix_select<ORD_A>(src, pr, one, (uint64_t)rp.top_k, sm);
-          pr.use_k = 1;
-        }
+    // compiler barrier: keep every load above issued here, before anything
+    // waits on the summaries (no hardware wait is implied)
+    asm volatile("" ::: "memory");
+    const float m = wmax_f(lane < G ? hd.m : -INFINITY);
+    const int flagged = wsum_i(lane < G ? hd.flags : 0);
+    int path;
+    if (rp.greedy) {
+      const int bi = wmin_i((lane < G && hd.m == m) ? hd.best_i : 0x7FFFFFFF);
+      if (flagged) {
+        path = 1;
       } else {
-        if (rp.use_p) apply_p(false);
-        if (!ambiguous && rp.use_m && !pr.none) apply_m();
-        if (!ambiguous && rp.use_k && !pr.none && count(pr) > rp.top_k) {
-          pr.ck = wave_radix_select<ORD_A>(src, pr, one, (uint64_t)rp.top_k, sm);
-          pr.use_k = 1;
-        }
-      }
-      if (ambiguous) {
-        fallback = 3;
-      } else {
-        // Draw: integer inverse CDF in vocabulary order over the kept candidates.
-        const float invT = (float)(1.0 / (double)rp.T);
-        const float Tc = (float)fmax((double)rp.T, 1e-5);
-        auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, Tc)); };
-        uint64_t zv = 0;
-        int nk = 0;
-        src.each([&](int i, float l) {
-          if (pr.keep(i, l)) { zv += vw(i, l); ++nk; }
-        });
-        const uint64_t ZV = wave_sum_u64(zv);
-        const int nkept = wave_sum_i(nk);
-        if (a.tokens) {
-          int tok = 0;
-          if (ZV) {
-            const uint64_t tgt = draw_target(ub, ZV);
-            tok = 0x3FFFF - (int)wave_radix_select<ORD_ID>(src, pr, vw, tgt + 1, sm);
-          }
-          if (lane == 0) a.tokens[b] = tok;
-        }
         if (lane == 0) {
-          if (a.kept) a.kept[b] = nkept;
-          P.path[b] = 0;
+          if (a.tokens) a.tokens[b] = bi == 0x7FFFFFFF ? 0 : bi;
+          if (a.kept) a.kept[b] = 1;
         }
-        float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
-        if (out) {
-          const double lz = log(ldexp((double)ZV, -44));
-          src.each([&](int i, float l) {
-            if (!pr.keep(i, l)) return;
-            out[i] = a.out_mode == WH_OUT_MASKED ? l : (float)((double)chain_scale(a.chain, l - m, invT, Tc) - lz);
-          });
-        }
+        path = 2;
       }
+    } else if (flagged || rp.all) {
+      path = 1;
+    } else {
+      const float tcov = wmax_f(lane < G ? hd.tau : -INFINITY);
+      const int nmax = wmax_i(lane < G ? hd.n : 0);
+      const int TS = (nmax + 63) / 64;
+      if (G * TS <= QM) path = merge_regs(a, P, b, rp, hd, G, m, tcov, ub, st, TS);
+      else path = merge_lds(&kernargs()->a, &kernargs()->p, b, rp, G, m, tcov, ub, dyn, &sm);
     }
-    if (lane == 0) s_fallback = fallback;
+    if (lane == 0) {
+      s_path = path;
+      P.path[b] = path;
+    }
   }
   __syncthreads();
-  if (s_fallback) {
-    if (tid == 0) P.path[b] = s_fallback == 3 ? 3 : 1;
-    exact_row(a, b, dyn, esm);
-  }
+  const int path = s_path;
+  if (path == 1 || path == 3) exact_row(kernargs()->a, b, dyn, esm);
 }
 
 // ---------------------------------------------------------------------------
 // Host side: plan, workspace layout, dispatch.
 // ---------------------------------------------------------------------------
 struct HostPlan {
-  int G, SL, R, cap, rule_cap, ept;
+  int G, SL, R, cap, rule_cap, ept, pcap, codes_bytes, cand_off;
+  size_t lds;
 };
 
-static HostPlan make_plan(int B, int V, int dtype) {
+static HostPlan make_plan(int B, int V, int dtype, int hcap) {
   HostPlan p;
   p.ept = dtype == WH_DTYPE_BF16 ? 8 : 4;
-  const int slmax = FT * p.ept * FAST_RMAX;
-  int g = std::max((256 + B - 1) / std::max(B, 1), (V + slmax - 1) / slmax);
-  g = std::min(g, 32);
-  p.G = g;
-  int sl = (V + g - 1) / g;
+  const int slmax = FT * FAST_NE;
+  const int bb = std::max(B, 1);
+  int g = std::max(std::min((256 + bb - 1) / bb, GPREF), (V + slmax - 1) / slmax);
+  p.G = std::max(g, 1);
+  int sl = (V + p.G - 1) / p.G;
   sl = (sl + p.ept - 1) / p.ept * p.ept;
   p.SL = sl;
   p.R = (sl + FT * p.ept - 1) / (FT * p.ept);
-  p.cap = std::min(2048, 16384 / g);
-  p.rule_cap = p.cap / 2;
+  p.cap = FAST_CAP;
+  p.rule_cap = FAST_CAP / 2;
+  p.codes_bytes = hcap > 0 ? (sl * 2 + 15) / 16 * 16 : 0;
+  p.pcap = (hcap > 0 && dtype == WH_DTYPE_BF16) ? std::min(hcap / 2, sl) : 0;
+  p.cand_off = p.codes_bytes + p.pcap * 8;
+  p.lds = (size_t)p.cand_off + (size_t)p.cap * sizeof(int2);
   return p;
 }
 
@@ -821,7 +1258,7 @@ struct WsLayout {
   size_t path, hdr, cand, total;
 };
 
-// Workspace: [path B x int32][slice headers B*G][candidates B*G*cap]
+// Workspace: [path B x int32][slice summaries B*G][candidates B*G*cap]
 static WsLayout ws_layout(int B, const HostPlan& p) {
   WsLayout w;
   w.path = 0;
@@ -833,8 +1270,8 @@ static WsLayout ws_layout(int B, const HostPlan& p) {
 
 size_t sample_workspace_bytes(int B, int V) {
   if (B <= 0 || V <= 0) return 256;
-  WsLayout a = ws_layout(B, make_plan(B, V, WH_DTYPE_F32));
-  WsLayout b = ws_layout(B, make_plan(B, V, WH_DTYPE_BF16));
+  WsLayout a = ws_layout(B, make_plan(B, V, WH_DTYPE_F32, 0));
+  WsLayout b = ws_layout(B, make_plan(B, V, WH_DTYPE_BF16, 0));
   return std::max(a.total, b.total);
 }
 
@@ -854,24 +1291,31 @@ static int launch_slice_t(const SampleKArgs& k, const FastPlan& fp, size_t lds, 
   return WH_OK;
 }
 
-// R is rounded up to an instantiated register count.
-template <int DT>
-static int launch_slice_dt(int R, const SampleKArgs& k, const FastPlan& fp, size_t lds, hipStream_t st) {
-  if (R <= 1) return launch_slice_t<DT, 1>(k, fp, lds, st);
-  if (R <= 2) return launch_slice_t<DT, 2>(k, fp, lds, st);
-  if (R <= 3) return launch_slice_t<DT, 3>(k, fp, lds, st);
-  if (R <= 4) return launch_slice_t<DT, 4>(k, fp, lds, st);
-  if (R <= 5) return launch_slice_t<DT, 5>(k, fp, lds, st);
-  if (R <= 6) return launch_slice_t<DT, 6>(k, fp, lds, st);
-  if (R <= 8) return launch_slice_t<DT, 8>(k, fp, lds, st);
-  if (R <= 10) return launch_slice_t<DT, 10>(k, fp, lds, st);
-  if (R <= 12) return launch_slice_t<DT, 12>(k, fp, lds, st);
-  return launch_slice_t<DT, 16>(k, fp, lds, st);
+// R (16-byte loads per thread) is rounded up to an instantiated value.
+static int launch_slice(int dtype, int R, const SampleKArgs& k, const FastPlan& fp, size_t lds, hipStream_t st) {
+  if (dtype == WH_DTYPE_BF16) {
+    switch (R) {
+      case 1: return launch_slice_t<1, 1>(k, fp, lds, st);
+      case 2: return launch_slice_t<1, 2>(k, fp, lds, st);
+      case 3: return launch_slice_t<1, 3>(k, fp, lds, st);
+      case 4: return launch_slice_t<1, 4>(k, fp, lds, st);
+      case 5: return launch_slice_t<1, 5>(k, fp, lds, st);
+      default: return launch_slice_t<1, 6>(k, fp, lds, st);
+    }
+  }
+  if (R <= 1) return launch_slice_t<0, 1>(k, fp, lds, st);
+  if (R <= 2) return launch_slice_t<0, 2>(k, fp, lds, st);
+  if (R <= 3) return launch_slice_t<0, 3>(k, fp, lds, st);
+  if (R <= 4) return launch_slice_t<0, 4>(k, fp, lds, st);
+  if (R <= 6) return launch_slice_t<0, 6>(k, fp, lds, st);
+  if (R <= 8) return launch_slice_t<0, 8>(k, fp, lds, st);
+  if (R <= 10) return launch_slice_t<0, 10>(k, fp, lds, st);
+  return launch_slice_t<0, 12>(k, fp, lds, st);
 }
 
 int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st) {
   const int esz = k0.dtype == WH_DTYPE_BF16 ? 2 : 4;
-  HostPlan hp = make_plan(k0.B, k0.V, k0.dtype);
+  HostPlan hp = make_plan(k0.B, k0.V, k0.dtype, k0.hcap);
   WsLayout wl = ws_layout(k0.B, hp);
   const bool aligned = ((uintptr_t)k0.logits % 16 == 0) && ((k0.row_stride * esz) % 16 == 0) && (k0.V % hp.ept == 0);
   if (!aligned || !p->workspace || p->workspace_bytes < wl.total) return launch_sample_exact(k0, st);
@@ -881,14 +1325,15 @@ int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st
   fp.SL = hp.SL;
   fp.cap = hp.cap;
   fp.rule_cap = hp.rule_cap;
+  fp.pcap = hp.pcap;
+  fp.codes_bytes = hp.codes_bytes;
+  fp.cand_off = hp.cand_off;
   char* ws = (char*)p->workspace;
   fp.path = (int*)(ws + wl.path);
   fp.hdr = (SliceHdr*)(ws + wl.hdr);
   fp.cand = (int2*)(ws + wl.cand);
-  const size_t lds_slice = cand_buf_offset(k.hcap, hp.SL) + (size_t)hp.cap * sizeof(int2);
   const size_t lds_merge = std::max((size_t)hp.G * hp.cap * 8, penalty_lds_bytes(k));
-  int rc = k.dtype == WH_DTYPE_BF16 ? launch_slice_dt<1>(hp.R, k, fp, lds_slice, st)
-                                    : launch_slice_dt<0>(hp.R, k, fp, lds_slice, st);
+  int rc = launch_slice(k.dtype, hp.R, k, fp, hp.lds, st);
   if (rc) return rc;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "slice_kernel launch failed: %s", hipGetErrorString(e));
