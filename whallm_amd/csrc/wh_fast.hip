@@ -10,12 +10,14 @@
 // short candidate list.  Every VALU op per element costs about a quarter of
 // a microsecond over a full batch, so the per-element work is only the
 // unpack and a max.  The rest is done per 16-byte group or per rare element:
-//   * Penalties.  The history window becomes a dense u16 code per slice
-//     element in LDS: the count in the frequency window, plus flags for the
-//     repetition and presence windows.  The thread holding a group reads that
-//     group's codes with one LDS load and recomputes the few penalised
-//     values.  A penalised bf16 value cannot live in the packed register, so
-//     it moves to a short LDS list and its register slot is set to -inf.
+//   * Penalties, worked from the history side (a few hundred ids per slice)
+//     rather than the element side: sparse penalised elements spread over
+//     every wave would make each wave run the penalty code.  The window
+//     becomes a dense u16 code per slice element in LDS (count in the
+//     frequency window, flags for the repetition and presence windows).  The
+//     first thread to touch an element's code computes its penalised value
+//     from a gathered raw logit and lists it.  The registers holding the
+//     element turn it into a NaN with one OR per 4-byte word.
 //   * The slice max m_s and the max of every 16-byte group.
 //   * The candidate threshold tau_s.  No kept element of the row can fall
 //     below it:
@@ -54,7 +56,12 @@ constexpr int FAST_NE = 48;       // logits per thread held in VGPRs, at most
 constexpr int GPREF = 4;          // slices per row preferred for small batches
 constexpr int FAST_CAP = 2048;    // candidate capacity per slice
 constexpr int RUNGS = 8;          // thresholds per ladder round
-constexpr int QM = 8;             // merge: candidate slots per lane
+constexpr int LADDER_ROUNDS = 4;  // ladder rounds at most (the first plus refinements)
+constexpr int QM = 16;            // merge: candidate slots per lane
+constexpr int QSPEC = 8;          // merge: slots loaded speculatively with the summaries (slices <= 8)
+constexpr int SORT_MAX = 512;     // slices with at most this many candidates write them sorted by id
+constexpr int HDR_OVERFLOW = 1;   // SliceHdr.flags: the row needs the exact engine
+constexpr int HDR_UNSORTED = 2;   // SliceHdr.flags: candidates not sorted by id
 constexpr float BAND1 = 1.5f;     // band floors below tau, nats
 constexpr float BAND2 = 3.5f;
 
@@ -62,7 +69,7 @@ struct SliceHdr {
   float m;        // slice max (penalised)
   float tau;      // every slice element >= tau is a candidate
   int n;          // candidates written
-  int flags;      // 1: candidate overflow or no usable bound -- the row needs the exact engine
+  int flags;      // HDR_OVERFLOW: overflow or no usable bound (exact engine); HDR_UNSORTED
   float t1, t2;   // band floors t1 = tau - 1.5, t2 = tau - 3.5
   int g1, g2;     // groups (or penalised elements) whose max lies in [t1, tau) / [t2, t1)
   int nall;       // elements in the slice
@@ -77,13 +84,13 @@ struct FastPlan {
   int SL;          // slice length (a multiple of the elements per 16-byte load)
   int cap;         // candidate capacity per slice
   int rule_cap;    // largest k a slice may bound
-  int pcap;        // capacity of the penalised-element list (bf16 with penalties)
+  int pcap;        // capacity of the penalised-element list (with penalties)
   int codes_bytes; // LDS bytes of the penalty codes (0 without penalties)
   int cand_off;    // LDS offset of the candidate buffer
   int* path;       // [B] 0: merged in registers, 4: merged through LDS, 1: exact engine
                    //     (overflow / no bound), 2: greedy, 3: exact engine (top-p cut unsettled)
   SliceHdr* hdr;   // [B * G]
-  int2* cand;      // [B * G * cap] (value bits, id)
+  int2* cand;      // [B * G * cap] (value bits, id), sorted by id unless HDR_UNSORTED
 };
 
 struct RowParams {
@@ -165,9 +172,6 @@ __device__ __forceinline__ float min_p_log(const SampleKArgs& a, float min_p) {
 __device__ __forceinline__ uint32_t comp(const uint4& v, int i) {
   return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
-__device__ __forceinline__ void set_comp(uint4& v, int i, uint32_t x) {
-  if (i == 0) v.x = x; else if (i == 1) v.y = x; else if (i == 2) v.z = x; else v.w = x;
-}
 template <int DT>
 __device__ __forceinline__ float elem(const uint4& v, int e) {
   if (DT == 0) return __uint_as_float(comp(v, e));
@@ -180,12 +184,6 @@ __device__ __forceinline__ float elem_n(const uint4& v, int e) {
   return elem<DT>(v, e) + 0.0f;
 }
 template <int DT>
-__device__ __forceinline__ void kill(uint4& v, int e) {
-  if (DT == 0) { set_comp(v, e, 0xFF800000u); return; }
-  const uint32_t x = comp(v, e >> 1);
-  set_comp(v, e >> 1, (e & 1) ? ((x & 0x0000FFFFu) | 0xFF800000u) : ((x & 0xFFFF0000u) | 0x0000FF80u));
-}
-template <int DT>
 __device__ __forceinline__ float grp_max(const uint4& v) {
   if (DT == 0)
     return fmaxf(fmaxf(__uint_as_float(v.x), __uint_as_float(v.y)), fmaxf(__uint_as_float(v.z), __uint_as_float(v.w)));
@@ -195,11 +193,6 @@ __device__ __forceinline__ float grp_max(const uint4& v) {
                         fmaxf(__uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u)));
   return fmaxf(a, c);
 }
-// u16 penalty code of element e of a group from its codes word(s).
-__device__ __forceinline__ uint32_t code_of(const uint4& cw, int e) {
-  return (comp(cw, e >> 1) >> ((e & 1) * 16)) & 0xFFFFu;
-}
-
 // Penalty code bits: count in the frequency window (bits 0-12, at most 4096),
 // in the repetition window (bit 13), in the presence window (bit 14).  A flag
 // whose window equals the frequency window is read from the count instead.
@@ -224,7 +217,7 @@ struct SliceSmem {
   int npatch;                   // penalised bf16 elements listed
   float redm[FNW];
   int redg[FNW];
-  int lad[3][RUNGS];            // ladder totals per round (zeroed at kernel start)
+  int lad[LADDER_ROUNDS][RUNGS];  // ladder totals per round (zeroed at kernel start)
   int redb[FNW][2];
   double redz[FNW];
 };
@@ -258,11 +251,12 @@ __device__ __forceinline__ void ladder_count(const float (&gm)[R], const int2* p
   for (int j = 0; j < RUNGS; ++j) tot[j] = sm.lad[buf][j];
 }
 
-// Candidate threshold from the ladder.
+// Candidate threshold from the ladder (rungs from the slice max down to 1024
+// nats below it, then refinements that split the bracketing interval).
 //   k > 0 (top-k bound): a threshold with at least k slice elements at or
 //     above it -- the highest rung whose group count reaches k (each counted
-//     group holds at least one such element), refined between rungs while the
-//     count exceeds half the buffer; -inf when no rung reaches k.
+//     group holds at least one such element), refined while the count
+//     exceeds max(2k, 64); -inf when no rung reaches k.
 //   k <= 0 (top-p alone): the lowest rung whose group count is at most half
 //     the buffer, refined once towards the next rung.
 template <int R>
@@ -270,7 +264,7 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
                                             SliceSmem& sm) {
   // Every rung array is indexed with compile-time indices only (unrolled
   // loops with selects), so it stays in registers.
-  const float D0[RUNGS] = {0.0f, 0.5f, 1.0f, 2.0f, 4.0f, 8.0f, 16.0f, 32.0f};
+  const float D0[RUNGS] = {0.0f, 0.5f, 1.0f, 2.0f, 4.0f, 16.0f, 128.0f, 1024.0f};
   const int half = cap / 2;
   float x[RUNGS];
   int c[RUNGS];
@@ -279,6 +273,7 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
   ladder_count<R>(gm, patch, npatch, x, c, 0, sm);
   if (k > 0) {
     // counts grow with j: hi = last rung with count < k, lo = first with >= k
+    const int target = max(2 * k, 64);
     bool found = false;
     float lo = -INFINITY, hi = INFINITY;
     int clo = 0;
@@ -292,7 +287,7 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
       if (!found) hi = x[j];
     }
     if (!found) return -INFINITY;
-    for (int round = 1; round < 3 && clo > half && hi != INFINITY; ++round) {
+    for (int round = 1; round < LADDER_ROUNDS && clo > target && hi != INFINITY; ++round) {
       const float span = hi - lo;
 #pragma unroll
       for (int q = 0; q < RUNGS; ++q) x[q] = hi - span * (float)(q + 1) / (float)(RUNGS + 1);
@@ -360,21 +355,24 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   //    first wait.
   const RowRaw raw = row_raw(a, b);
   const bool pen = a.hcap > 0;
-  constexpr int HPF = 4;
+  constexpr int HPF = 4;  // history positions per thread: HPF * FT >= WH_MAX_WINDOW
   const int hs = (int)a.hist_stride;
-  const bool pf = hs <= HPF * FT;
+  const bool pf = hs <= HPF * FT;  // the whole history row fits the prefetch
   int hreg[HPF];
-  int len = 0;
+  int len = 0, jbase = 0;
 #pragma unroll
   for (int q = 0; q < HPF; ++q) hreg[q] = -1;
   // Every vector load is unconditional, from a clamped in-bounds address, so
   // the number of loads in flight is the same on every path and each wait is
   // for exactly the loads it needs.
+  const int32_t* hrow = a.hist + (long long)b * a.hist_stride;
   if (pen) {
-    const int32_t* h = a.hist + (long long)b * a.hist_stride;
+    len = max(0, min(*(cint*)(a.hist_len + b), hs));
+    // rows longer than the prefetch read the last HPF * FT positions (every
+    // window is a suffix of at most WH_MAX_WINDOW ids)
+    if (!pf) jbase = max(0, len - HPF * FT);
 #pragma unroll
-    for (int q = 0; q < HPF; ++q) hreg[q] = h[min(tid + q * FT, hs - 1)];
-    len = *(cint*)(a.hist_len + b);
+    for (int q = 0; q < HPF; ++q) hreg[q] = hrow[min(jbase + tid + q * FT, hs - 1)];
   }
   const char* rowp = (const char*)a.logits + (size_t)b * a.row_stride * ESZ;
   uint4 d[R];
@@ -387,33 +385,35 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   const RowParams rp = row_params(a, raw, P.rule_cap);
   SliceHdr* hdr = P.hdr + (long long)b * P.G + s;
   if (rp.all) {
-    if (tid == 0) hdr->flags = 1;
+    if (tid == 0) hdr->flags = HDR_OVERFLOW;
     return;
   }
   float* out = a.out_rows ? a.out_rows + (long long)b * V : nullptr;
-  if (tid < 3 * RUNGS) (&sm.lad[0][0])[tid] = 0;
+  if (tid < LADDER_ROUNDS * RUNGS) (&sm.lad[0][0])[tid] = 0;
   if (tid == 0) {
     sm.cnt = 0;
     sm.npatch = 0;
   }
 
-  // 2. penalties: dense per-element codes in LDS, applied by the thread that
-  //    holds the element.  The history row (up to 4 ids per thread) and its
-  //    length are fetched together with the logits.
+  // 2. penalties, from the history side.  Each in-window id of this slice is
+  //    entered in a dense u16 code per slice element (count in the frequency
+  //    window, repetition / presence flags); the thread whose atomic first
+  //    touches an element owns it.  Owners turn their element's final code and
+  //    raw logit (a gather from the row, issued as soon as the ids arrive) into
+  //    the penalised value, list it, and set the code to 0xFFFF.  The threads
+  //    holding the logits then OR the codes into their registers: a penalised
+  //    element becomes NaN there, which every max and >= test ignores, and it
+  //    lives on only in the list.
   uint32_t* codes = (uint32_t*)dyn;
+  uint16_t* codes16 = (uint16_t*)dyn;
   int2* patch = (int2*)(dyn + P.codes_bytes);
   int2* cbuf = (int2*)(dyn + P.cand_off);
   float pmax = -INFINITY;
-  PenCtx pc;
-  pc.on_r = pc.on_p = pc.on_f = pc.dr = pc.dp = false;
-  pc.rep = a.rep;
-  pc.pres = a.pres;
-  pc.freq = a.freq;
   if (pen) {
-    const int32_t* h = a.hist + (long long)b * a.hist_stride;
-    const int words = P.codes_bytes / 16;
-    for (int w = tid; w < words; w += FT) ((uint4*)codes)[w] = make_uint4(0u, 0u, 0u, 0u);
-    len = max(0, min(len, hs));
+    PenCtx pc;
+    pc.rep = a.rep;
+    pc.pres = a.pres;
+    pc.freq = a.freq;
     pc.on_r = a.rep != 0.0f;
     pc.on_p = a.pres != 0.0f;
     pc.on_f = a.freq != 0.0f;
@@ -424,24 +424,50 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     pc.dr = pc.on_r && pc.on_f && wr == wf;
     pc.dp = pc.on_p && pc.on_f && wp == wf;
     const int W = max(wr, max(wp, wf));
-    auto insert = [&](int j, int t) {
-      if (t < v0 || t >= v1) return;
-      const int o = t - v0;
+    const int words = P.codes_bytes / 16;
+    for (int w = tid; w < words; w += FT) ((uint4*)codes)[w] = make_uint4(0u, 0u, 0u, 0u);
+    bool inw[HPF];
+    uint32_t rawv[HPF];
+#pragma unroll
+    for (int q = 0; q < HPF; ++q) {
+      const int j = jbase + tid + q * FT;
+      const int t = hreg[q];
+      inw[q] = j >= len - W && j < len && t >= v0 && t < v1;
+      const int tc = min(max(t, v0), v1 - 1);
+      rawv[q] = DT ? (uint32_t)*(const uint16_t*)(rowp + (size_t)tc * 2) : *(const uint32_t*)(rowp + (size_t)tc * 4);
+    }
+    __syncthreads();
+    uint32_t own = 0;
+#pragma unroll
+    for (int q = 0; q < HPF; ++q) {
+      if (!inw[q]) continue;
+      const int j = jbase + tid + q * FT;
+      const int o = hreg[q] - v0;
       const int sh = (o & 1) * 16;
       const uint32_t add = (pc.on_f && j >= len - wf) ? 1u : 0u;
       const uint32_t fl = ((pc.on_r && !pc.dr && j >= len - wr) ? PEN_R : 0u) | ((pc.on_p && !pc.dp && j >= len - wp) ? PEN_P : 0u);
-      if (add) atomicAdd(&codes[o >> 1], add << sh);
-      if (fl) atomicOr(&codes[o >> 1], fl << sh);
-    };
-    __syncthreads();
-    if (pf) {
-#pragma unroll
-      for (int q = 0; q < HPF; ++q) {
-        const int j = tid + q * FT;
-        if (j >= len - W && j < len) insert(j, hreg[q]);  // len <= hs, so j < hs
+      // the first read-modify-write of the element's code sees 0 (every
+      // update leaves it non-zero): that thread owns the element
+      uint32_t old = 0xFFFFFFFFu;
+      if (add) old = atomicAdd(&codes[o >> 1], add << sh);
+      if (fl) {
+        const uint32_t o2 = atomicOr(&codes[o >> 1], fl << sh);
+        if (!add) old = o2;
       }
-    } else {
-      for (int j = len - W + tid; j < len; j += FT) insert(j, h[j]);
+      if (((old >> sh) & 0xFFFFu) == 0u) own |= 1u << q;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < HPF; ++q) {
+      if (!((own >> q) & 1u)) continue;
+      const int t = hreg[q];
+      const uint32_t code = codes16[t - v0];
+      const float l = (DT ? __uint_as_float(rawv[q] << 16) : __uint_as_float(rawv[q])) + 0.0f;
+      const float v = pc.apply(l, code);
+      const int slot = atomicAdd(&sm.npatch, 1);
+      if (slot < P.pcap) patch[slot] = make_int2(__float_as_int(v), t);
+      codes16[t - v0] = 0xFFFFu;
+      pmax = fmaxf(pmax, v);
     }
     __syncthreads();
 #pragma unroll
@@ -449,28 +475,18 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
       const int g = v0 + (r * FT + tid) * EPT;
       if (g < v1) {
         const char* cp = (const char*)codes + (size_t)(g - v0) * 2;
-        uint4 cw;
         if (DT) {
-          cw = *(const uint4*)cp;
+          const uint4 cw = *(const uint4*)cp;
+          d[r].x |= cw.x;
+          d[r].y |= cw.y;
+          d[r].z |= cw.z;
+          d[r].w |= cw.w;
         } else {
-          const uint2 c2 = *(const uint2*)cp;
-          cw = make_uint4(c2.x, c2.y, 0u, 0u);
-        }
-        if ((cw.x | cw.y | cw.z | cw.w) != 0u) {
-#pragma unroll
-          for (int e = 0; e < EPT; ++e) {
-            const uint32_t code = code_of(cw, e);
-            if (!code) continue;
-            const float v = pc.apply(elem_n<DT>(d[r], e), code);
-            if (DT) {
-              const int slot = atomicAdd(&sm.npatch, 1);
-              if (slot < P.pcap) patch[slot] = make_int2(__float_as_int(v), g + e);
-              kill<DT>(d[r], e);
-              pmax = fmaxf(pmax, v);
-            } else {
-              set_comp(d[r], e, __float_as_uint(v));
-            }
-          }
+          const uint2 cw = *(const uint2*)cp;
+          d[r].x |= (cw.x & 0xFFFFu) * 0x10001u;
+          d[r].y |= (cw.x >> 16) * 0x10001u;
+          d[r].z |= (cw.y & 0xFFFFu) * 0x10001u;
+          d[r].w |= (cw.y >> 16) * 0x10001u;
         }
       }
     }
@@ -530,7 +546,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
       for (int w = 1; w < FNW; ++w) best = min(best, sm.redg[w]);
       hdr->m = ms;
       hdr->best_i = best;
-      hdr->flags = npatch_raw > P.pcap ? 1 : 0;
+      hdr->flags = npatch_raw > P.pcap ? HDR_OVERFLOW : 0;
       hdr->n = 0;
     }
     return;
@@ -557,12 +573,10 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     n2 += (x >= t2 && !(x >= t1)) ? 1 : 0;
     if (x >= tau) {
       const int g = v0 + (r * FT + tid) * EPT;
-      uint4 cw = make_uint4(0u, 0u, 0u, 0u);
-      if (DT && pen && g < v1) cw = *(const uint4*)((const char*)codes + (size_t)(g - v0) * 2);
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
         const float l = elem_n<DT>(d[r], e);
-        if (l >= tau && g + e < v1 && !(DT && code_of(cw, e))) {
+        if (l >= tau && g + e < v1) {  // penalised elements are NaN here
           const int slot = atomicAdd(&sm.cnt, 1);
           if (slot < P.cap) cbuf[slot] = make_int2(__float_as_int(l), g + e);
         }
@@ -570,7 +584,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     }
     if (need_zf) {
 #pragma unroll
-      for (int e = 0; e < EPT; ++e) zs += __expf(elem<DT>(d[r], e) - ms);
+      for (int e = 0; e < EPT; ++e) zs += __expf(fmaxf(elem<DT>(d[r], e), -INFINITY) - ms);  // NaN (penalised) -> 0
     }
   }
   for (int p = tid; p < npatch; p += FT) {
@@ -595,7 +609,18 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   const int n = sm.cnt;
   const int nw = min(n, P.cap);
   int2* gc = P.cand + ((long long)b * P.G + s) * P.cap;
-  for (int j = tid; j < nw; j += FT) gc[j] = cbuf[j];
+  const bool sorted = nw <= SORT_MAX;
+  if (sorted) {
+    // ids are unique within a slice: each candidate's rank by id is its slot
+    for (int j = tid; j < nw; j += FT) {
+      const int2 c = cbuf[j];
+      int r = 0;
+      for (int i = 0; i < nw; ++i) r += cbuf[i].y < c.y ? 1 : 0;
+      gc[r] = c;
+    }
+  } else {
+    for (int j = tid; j < nw; j += FT) gc[j] = cbuf[j];
+  }
   if (out) {
     // non-candidates are never kept; the merge writes the kept ones
 #pragma unroll
@@ -618,7 +643,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     hdr->m = ms;
     hdr->tau = tau;
     hdr->n = nw;
-    hdr->flags = (n > P.cap || npatch_raw > P.pcap) ? 1 : 0;
+    hdr->flags = ((n > P.cap || npatch_raw > P.pcap) ? HDR_OVERFLOW : 0) | (sorted ? 0 : HDR_UNSORTED);
     hdr->t1 = t1;
     hdr->t2 = t2;
     hdr->g1 = s1;
@@ -655,13 +680,15 @@ __device__ __forceinline__ ZBounds z_bounds(const SliceHdr& hd, bool own, float 
   double lo = 0.0, hi = 0.0, zl = 0.0, zh = 0.0;
   int no_zf = 0;
   if (own && hd.m != -INFINITY) {
+    // float exponentials: their error (a few ulp, arguments <= 0) is far
+    // inside EPS
     auto wlo = [&](float t) {
-      return t == -INFINITY ? 0.0 : fmax(floor(exp((double)t - (double)m) * SC * (1.0 - EPS)) - 1.0, 0.0);
+      return t == -INFINITY ? 0.0 : fmax(floor((double)expf(t - m) * SC * (1.0 - EPS)) - 1.0, 0.0);
     };
     lo = (double)hd.g1 * wlo(hd.t1) + (double)hd.g2 * wlo(hd.t2);
-    hi = (double)(hd.nall - hd.n) * (exp((double)hd.tau - (double)m) * SC * (1.0 + EPS) + 1.0);
+    hi = (double)(hd.nall - hd.n) * ((double)expf(hd.tau - m) * SC * (1.0 + EPS) + 1.0);
     if (hd.zf >= 0.0) {
-      const double sc = exp((double)hd.m - (double)m) * SC;
+      const double sc = (double)expf(hd.m - m) * SC;
       zl = hd.zf * sc * (1.0 - EPS) - (double)hd.nall;
       zh = hd.zf * sc * (1.0 + EPS) + (double)hd.nall;
     } else {
@@ -699,6 +726,17 @@ __device__ __forceinline__ uint32_t common_prefix(uint32_t lo, uint32_t hi, int&
   d |= d >> 16;
   nbits = __popc(d);
   return lo & ~d;
+}
+
+// Inclusive prefix sum over the wave's lanes (lane order).
+__device__ __forceinline__ uint64_t wscan_u64(uint64_t x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x;
 }
 
 // Candidates in registers: QM slots per lane, alive bits in `al`.
@@ -1046,7 +1084,7 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& 
     st.al |= valid ? (1u << t) : 0u;
   }
 #pragma unroll
-  for (int t = 0; t < QM; ++t) st.w[t] = st.on(t) ? exp_fix44(st.cl[t] - m) : 0ull;
+  for (int t = 0; t < QM; ++t) st.w[t] = (t < G * TS && st.on(t)) ? exp_fix44(st.cl[t] - m) : 0ull;
   const uint64_t Scand = st.mass(false, 0.0f);
   const ZBounds zb = z_bounds(hd, lane < G, m, Scand);
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
@@ -1056,24 +1094,55 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& 
   const float Tc = (float)fmax((double)rp.T, 1e-5);
   if (rp.T != 1.0f) {
 #pragma unroll
-    for (int t = 0; t < QM; ++t) st.w[t] = st.on(t) ? exp_fix44(chain_scale(a.chain, st.cl[t] - m, invT, Tc)) : 0ull;
+    for (int t = 0; t < QM; ++t)
+      st.w[t] = (t < G * TS && st.on(t)) ? exp_fix44(chain_scale(a.chain, st.cl[t] - m, invT, Tc)) : 0ull;
   }
-  const uint64_t ZV = st.mass(false, 0.0f);
+  // Each slice's candidates are sorted by id and slot t holds chunk t / G of
+  // slice t % G, so vocabulary order is (slice, chunk, lane).  The slot
+  // totals in that order locate the slot holding the target; one prefix scan
+  // of that slot then gives the first kept element whose inclusive sum
+  // exceeds it.
+  const int GT = G * TS;
+  uint64_t tot[QM];
+#pragma unroll
+  for (int t = 0; t < QM; ++t) tot[t] = t < GT ? wsum_u64(st.on(t) ? st.w[t] : 0ull) : 0ull;
+  uint64_t ZV = 0;
+#pragma unroll
+  for (int t = 0; t < QM; ++t) ZV += tot[t];
   const int nkept = st.count();
   if (a.tokens) {
     int tok = 0;
     if (ZV) {
       const uint64_t tgt = draw_target(ub, ZV);
-      uint32_t imn, imx;
-      st.id_range([](int) { return true; }, imn, imx);
-      int ni;
-      uint32_t x = common_prefix(imn, imx, ni);
-      // largest x with sum_{kept, id < x} w <= tgt: the drawn id
-      for (int bit = ni - 1; bit >= 0; --bit) {
-        const uint32_t tr = x | (1u << bit);
-        if (st.mass_if([&](int t) { return (uint32_t)st.ci[t] < tr; }) <= tgt) x = tr;
-      }
-      tok = (int)x;
+      // walk the slots in (slice, chunk) order
+      uint64_t before = 0;
+      int ts = -1;
+      uint64_t rem = 0;
+      for (int sl = 0; sl < G && ts < 0; ++sl)
+        for (int ch = 0; ch < TS && ts < 0; ++ch) {
+          const int t = ch * G + sl;
+          uint64_t tt = 0;
+#pragma unroll
+          for (int u2 = 0; u2 < QM; ++u2) tt = u2 == t ? tot[u2] : tt;
+          if (before + tt > tgt) {
+            ts = t;
+            rem = tgt - before;
+          }
+          before += tt;
+        }
+      uint64_t wv = 0;
+      int iv = 0;
+      bool ov = false;
+#pragma unroll
+      for (int t = 0; t < QM; ++t)
+        if (t == ts) {
+          wv = st.on(t) ? st.w[t] : 0ull;
+          iv = st.ci[t];
+          ov = st.on(t);
+        }
+      const uint64_t incl = wscan_u64(wv);
+      const uint64_t hit = __ballot(ov && incl > rem);
+      if (hit) tok = (int)lane_u32((uint32_t)iv, (int)__ffsll((long long)hit) - 1);
     }
     if (lane == 0) a.tokens[b] = tok;
   }
@@ -1165,7 +1234,7 @@ __device__ __noinline__ int merge_lds(const SampleKArgs* ap, const FastPlan* pp,
 }
 
 
-__global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) {
+__global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ ExactSmem esm;
   __shared__ MergeSmem sm;
@@ -1186,7 +1255,8 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
     RegStore st;
 #pragma unroll
     for (int t = 0; t < QM; ++t) {
-      const int2 c = P.cand[((long long)b * G + min(t, G - 1)) * P.cap + lane];
+      int2 c = make_int2(0, -1);
+      if (t < QSPEC) c = P.cand[((long long)b * G + min(t, G - 1)) * P.cap + lane];
       st.cl[t] = __int_as_float(c.x);
       st.ci[t] = c.y;
     }
@@ -1194,7 +1264,8 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
     // waits on the summaries (no hardware wait is implied)
     asm volatile("" ::: "memory");
     const float m = wmax_f(lane < G ? hd.m : -INFINITY);
-    const int flagged = wsum_i(lane < G ? hd.flags : 0);
+    const int flagged = wsum_i(lane < G ? (hd.flags & HDR_OVERFLOW) : 0);
+    const int unsorted = wsum_i(lane < G ? (hd.flags & HDR_UNSORTED) : 0);
     int path;
     if (rp.greedy) {
       const int bi = wmin_i((lane < G && hd.m == m) ? hd.best_i : 0x7FFFFFFF);
@@ -1213,7 +1284,7 @@ __global__ void __launch_bounds__(1024) merge_kernel(SampleKArgs a, FastPlan P) 
       const float tcov = wmax_f(lane < G ? hd.tau : -INFINITY);
       const int nmax = wmax_i(lane < G ? hd.n : 0);
       const int TS = (nmax + 63) / 64;
-      if (G * TS <= QM) path = merge_regs(a, P, b, rp, hd, G, m, tcov, ub, st, TS);
+      if (G * TS <= QM && G <= QSPEC && !unsorted) path = merge_regs(a, P, b, rp, hd, G, m, tcov, ub, st, TS);
       else path = merge_lds(&kernargs()->a, &kernargs()->p, b, rp, G, m, tcov, ub, dyn, &sm);
     }
     if (lane == 0) {
@@ -1248,7 +1319,7 @@ static HostPlan make_plan(int B, int V, int dtype, int hcap) {
   p.cap = FAST_CAP;
   p.rule_cap = FAST_CAP / 2;
   p.codes_bytes = hcap > 0 ? (sl * 2 + 15) / 16 * 16 : 0;
-  p.pcap = (hcap > 0 && dtype == WH_DTYPE_BF16) ? std::min(hcap / 2, sl) : 0;
+  p.pcap = hcap > 0 ? std::min(hcap / 2, sl) : 0;
   p.cand_off = p.codes_bytes + p.pcap * 8;
   p.lds = (size_t)p.cand_off + (size_t)p.cap * sizeof(int2);
   return p;
@@ -1339,7 +1410,7 @@ int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st
   if (e != hipSuccess) return fail(WH_EHIP, "slice_kernel launch failed: %s", hipGetErrorString(e));
   rc = set_lds((const void*)merge_kernel, lds_merge);
   if (rc) return rc;
-  hipLaunchKernelGGL(merge_kernel, dim3(k.B), dim3(1024), lds_merge, st, k, fp);
+  hipLaunchKernelGGL(merge_kernel, dim3(k.B), dim3(512), lds_merge, st, k, fp);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "merge_kernel launch failed: %s", hipGetErrorString(e));
   return WH_OK;

@@ -176,14 +176,23 @@ __device__ uint64_t radix_select(const Src& src, const Pred& pr, Meas meas, uint
       if (w) atomicAdd((unsigned long long*)&sm.hist[(c >> shift) & 1023], (unsigned long long)w);
     });
     __syncthreads();
-    // suffix sums from the top bin: thread t owns bin 1023 - t
-    const int bin = 1023 - tid;
-    uint64_t hv = sm.hist[bin];
+    // suffix sums from the top bin: thread t owns the 1024 / blockDim bins
+    // 1023 - t * per .. 1024 - (t + 1) * per, in descending order
+    const int per = 1024 / (int)blockDim.x;
+    const int top = 1023 - tid * per;
+    uint64_t ls = 0;
+    for (int q = 0; q < per; ++q) ls += sm.hist[top - q];
     uint64_t tot;
-    uint64_t excl = block_exclusive_scan_u64(hv, sm.scratch64, &tot);
-    if (excl < target && excl + hv >= target) {
-      sm.bcast64[0] = (uint64_t)bin;
-      sm.bcast64[1] = excl;
+    uint64_t c = block_exclusive_scan_u64(ls, sm.scratch64, &tot);
+    if (c < target && c + ls >= target) {
+      for (int q = 0; q < per; ++q) {
+        const uint64_t hv = sm.hist[top - q];
+        if (c < target && c + hv >= target) {
+          sm.bcast64[0] = (uint64_t)(top - q);
+          sm.bcast64[1] = c;
+        }
+        c += hv;
+      }
     }
     __syncthreads();
     prefix = (prefix << 10) | sm.bcast64[0];
@@ -197,7 +206,8 @@ __device__ __forceinline__ float chain_scale(int chain, float d, float invT, flo
   return chain == WH_CHAIN_MLX ? d * invT : d / Tc;
 }
 
-// The whole exact algorithm for row b by one 1024-thread workgroup.
+// The whole exact algorithm for row b by one workgroup (64..1024 threads, a
+// power of two).
 __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_smem, ExactSmem& sm) {
   const int tid = threadIdx.x, nt = blockDim.x;
   const int V = a.V;

@@ -161,6 +161,57 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
     return tokens if len(res) == 1 else tuple(res)
 
 
+class SampleCall:
+    """A wh_sample launch bound to fixed device buffers.
+
+    For decode loops that refill the same logits / history / uniform buffers
+    every step: the C argument struct is built once, and each call is one
+    ctypes call into wh_sample on the stream current at construction.  Takes
+    the keyword arguments of sample(); `uniforms` is required (a buffer the
+    caller refills) and the outputs are the attributes `tokens` (and `kept`
+    with return_kept).
+    """
+
+    def __init__(self, logits: torch.Tensor, *, uniforms: torch.Tensor, temperature: float = 0.0,
+                 top_p: float = 1.0, top_k: int = 0, min_p: float = 0.0, chain="mlx", history=None,
+                 history_len=None, repetition_penalty: float = 0.0, presence_penalty: float = 0.0,
+                 frequency_penalty: float = 0.0, repetition_context: int = 20, presence_context: int = 20,
+                 frequency_context: int = 20, temperature_rows=None, top_p_rows=None, min_p_rows=None,
+                 top_k_rows=None, return_kept: bool = False, engine: str = "auto"):
+        logits, dt = _as_rows(logits)
+        L.require_device(logits)
+        B, V = logits.shape
+        dev = logits.device
+        rows = (_rows_param(temperature_rows, B, torch.float32, dev), _rows_param(top_p_rows, B, torch.float32, dev),
+                _rows_param(min_p_rows, B, torch.float32, dev), _rows_param(top_k_rows, B, torch.int32, dev))
+        u = torch.as_tensor(uniforms, dtype=torch.float32, device=dev).reshape(B)
+        if not u.is_contiguous():
+            raise ValueError("uniforms must be a contiguous [B] float32 buffer")
+        self.tokens = torch.empty(B, dtype=torch.int32, device=dev)
+        self.kept = torch.empty(B, dtype=torch.int32, device=dev) if return_kept else None
+        self.args = L.SampleArgs()
+        keep = _fill_args(self.args, logits, dt, chain, history, history_len, temperature, top_p, top_k, min_p,
+                          repetition_penalty, presence_penalty, frequency_penalty, repetition_context,
+                          presence_context, frequency_context, rows)
+        self.args.uniforms = u.data_ptr()
+        self.args.tokens = self.tokens.data_ptr()
+        self.args.kept_count = L.ptr(self.kept)
+        self.args.out_mode = L.OUT_LOGPROBS
+        self._ws = None
+        if engine != "exact":
+            self._ws = L.workspace(dev, L.lib().wh_sample_workspace_bytes(B, V))
+            self.args.workspace = self._ws.data_ptr()
+            self.args.workspace_bytes = self._ws.numel()
+        self._alive = (logits, u, rows, keep)
+        self._stream = ctypes.c_void_p(L.stream_of(logits))
+        self._fn = L.lib().wh_sample
+        self._ref = ctypes.byref(self.args)
+
+    def __call__(self) -> torch.Tensor:
+        L.check(self._fn(self._ref, self._stream))
+        return self.tokens
+
+
 def last_paths(device, B: int) -> torch.Tensor:
     """Per-row engine path of the last sliced-engine call on the current
     stream's workspace: 0 merged from candidates, 1 exact engine (candidate
