@@ -185,6 +185,24 @@ __device__ __forceinline__ double wsum_f64(double v) {
     return (uint64_t)__double_as_longlong(__longlong_as_double((long long)a) + __longlong_as_double((long long)b));
   }));
 }
+// K independent u64 sums reduced together: the DPP steps of the K chains
+// interleave, so their latencies overlap.
+template <int K>
+__device__ __forceinline__ void wsum_u64_k(uint64_t (&v)[K]) {
+#define WH_DPPK_STEP(C)                                                                              \
+  _Pragma("unroll") for (int k_ = 0; k_ < K; ++k_) {                                                 \
+    const uint64_t y_ = ((uint64_t)dpp32<C>((uint32_t)(v[k_] >> 32)) << 32) | dpp32<C>((uint32_t)v[k_]); \
+    v[k_] += y_;                                                                                     \
+  }
+  WH_DPPK_STEP(0xB1)
+  WH_DPPK_STEP(0x4E)
+  WH_DPPK_STEP(0x141)
+  WH_DPPK_STEP(0x140)
+#undef WH_DPPK_STEP
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = (lane_u64(v[k], 0) + lane_u64(v[k], 16)) + (lane_u64(v[k], 32) + lane_u64(v[k], 48));
+}
+
 // Number of lanes (of the active ones) where p holds; wave uniform.
 __device__ __forceinline__ int ballot_count(bool p) { return (int)__popcll(__ballot(p)); }
 

@@ -59,9 +59,7 @@ constexpr int RUNGS = 8;          // thresholds per ladder round
 constexpr int LADDER_ROUNDS = 4;  // ladder rounds at most (the first plus refinements)
 constexpr int QM = 16;            // merge: candidate slots per lane
 constexpr int QSPEC = 8;          // merge: slots loaded speculatively with the summaries (slices <= 8)
-constexpr int SORT_MAX = 512;     // slices with at most this many candidates write them sorted by id
 constexpr int HDR_OVERFLOW = 1;   // SliceHdr.flags: the row needs the exact engine
-constexpr int HDR_UNSORTED = 2;   // SliceHdr.flags: candidates not sorted by id
 constexpr float BAND1 = 1.5f;     // band floors below tau, nats
 constexpr float BAND2 = 3.5f;
 
@@ -69,7 +67,7 @@ struct SliceHdr {
   float m;        // slice max (penalised)
   float tau;      // every slice element >= tau is a candidate
   int n;          // candidates written
-  int flags;      // HDR_OVERFLOW: overflow or no usable bound (exact engine); HDR_UNSORTED
+  int flags;      // HDR_OVERFLOW: overflow or no usable bound (exact engine)
   float t1, t2;   // band floors t1 = tau - 1.5, t2 = tau - 3.5
   int g1, g2;     // groups (or penalised elements) whose max lies in [t1, tau) / [t2, t1)
   int nall;       // elements in the slice
@@ -90,7 +88,7 @@ struct FastPlan {
   int* path;       // [B] 0: merged in registers, 4: merged through LDS, 1: exact engine
                    //     (overflow / no bound), 2: greedy, 3: exact engine (top-p cut unsettled)
   SliceHdr* hdr;   // [B * G]
-  int2* cand;      // [B * G * cap] (value bits, id), sorted by id unless HDR_UNSORTED
+  int2* cand;      // [B * G * cap] (value bits, id), in no particular order
 };
 
 struct RowParams {
@@ -541,13 +539,14 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     __syncthreads();
     if (out)
       for (int p = tid; p < npatch; p += FT) out[patch[p].y] = __int_as_float(patch[p].x);
-    if (tid == 0) {
-      int best = sm.redg[0];
-      for (int w = 1; w < FNW; ++w) best = min(best, sm.redg[w]);
-      hdr->m = ms;
-      hdr->best_i = best;
-      hdr->flags = npatch_raw > P.pcap ? HDR_OVERFLOW : 0;
-      hdr->n = 0;
+    if (wv == 0) {
+      const int best = wmin_i(lane < FNW ? sm.redg[lane & (FNW - 1)] : 0x7FFFFFFF);
+      if (lane == 0) {
+        hdr->m = ms;
+        hdr->best_i = best;
+        hdr->flags = npatch_raw > P.pcap ? HDR_OVERFLOW : 0;
+        hdr->n = 0;
+      }
     }
     return;
   }
@@ -571,14 +570,19 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     const float x = gm[r];
     n1 += (x >= t1 && !(x >= tau)) ? 1 : 0;
     n2 += (x >= t2 && !(x >= t1)) ? 1 : 0;
-    if (x >= tau) {
-      const int g = v0 + (r * FT + tid) * EPT;
+    const int g = v0 + (r * FT + tid) * EPT;
+    if (x >= tau && g < v1) {
+      // one LDS atomic reserves the group's slots (penalised elements are NaN
+      // here and fail the test; a group lies wholly inside or outside the slice)
+      uint32_t msk = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) msk |= (elem<DT>(d[r], e) >= tau) ? (1u << e) : 0u;
+      int slot = atomicAdd(&sm.cnt, (int)__popc(msk));
 #pragma unroll
       for (int e = 0; e < EPT; ++e) {
-        const float l = elem_n<DT>(d[r], e);
-        if (l >= tau && g + e < v1) {  // penalised elements are NaN here
-          const int slot = atomicAdd(&sm.cnt, 1);
-          if (slot < P.cap) cbuf[slot] = make_int2(__float_as_int(l), g + e);
+        if ((msk >> e) & 1u) {
+          if (slot < P.cap) cbuf[slot] = make_int2(__float_as_int(elem_n<DT>(d[r], e)), g + e);
+          ++slot;
         }
       }
     }
@@ -609,18 +613,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   const int n = sm.cnt;
   const int nw = min(n, P.cap);
   int2* gc = P.cand + ((long long)b * P.G + s) * P.cap;
-  const bool sorted = nw <= SORT_MAX;
-  if (sorted) {
-    // ids are unique within a slice: each candidate's rank by id is its slot
-    for (int j = tid; j < nw; j += FT) {
-      const int2 c = cbuf[j];
-      int r = 0;
-      for (int i = 0; i < nw; ++i) r += cbuf[i].y < c.y ? 1 : 0;
-      gc[r] = c;
-    }
-  } else {
-    for (int j = tid; j < nw; j += FT) gc[j] = cbuf[j];
-  }
+  for (int j = tid; j < nw; j += FT) gc[j] = cbuf[j];
   if (out) {
     // non-candidates are never kept; the merge writes the kept ones
 #pragma unroll
@@ -632,18 +625,17 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
       }
     }
   }
-  if (tid == 0) {
-    int s1 = 0, s2 = 0;
-    double sz = 0.0;
-    for (int w = 0; w < FNW; ++w) {
-      s1 += sm.redb[w][0];
-      s2 += sm.redb[w][1];
-      sz += sm.redz[w];
-    }
+  if (wv == 0) {
+    // lanes 0..15 read one wave's partials each; DPP sums finish them
+    const bool lw = lane < FNW;
+    const int s1 = wsum_i(lw ? sm.redb[lane & (FNW - 1)][0] : 0);
+    const int s2 = wsum_i(lw ? sm.redb[lane & (FNW - 1)][1] : 0);
+    const double sz = need_zf ? wsum_f64(lw ? sm.redz[lane & (FNW - 1)] : 0.0) : 0.0;
+    if (lane == 0) {
     hdr->m = ms;
     hdr->tau = tau;
     hdr->n = nw;
-    hdr->flags = ((n > P.cap || npatch_raw > P.pcap) ? HDR_OVERFLOW : 0) | (sorted ? 0 : HDR_UNSORTED);
+    hdr->flags = (n > P.cap || npatch_raw > P.pcap) ? HDR_OVERFLOW : 0;
     hdr->t1 = t1;
     hdr->t2 = t2;
     hdr->g1 = s1;
@@ -651,6 +643,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     hdr->nall = v1 - v0;
     hdr->best_i = 0;
     hdr->zf = need_zf ? sz : -1.0;
+    }
   }
 }
 
@@ -675,6 +668,7 @@ struct ZBounds {
 //  * When every slice carries its float sum zf (hardware exp, relative error
 //    far below eps = 2e-4 for every term that exp_fix44 does not flush to 0),
 //    both bounds are also taken from zf.
+template <int G>
 __device__ __forceinline__ ZBounds z_bounds(const SliceHdr& hd, bool own, float m, uint64_t Scand) {
   const double SC = 17592186044416.0, EPS = 2e-4;
   double lo = 0.0, hi = 0.0, zl = 0.0, zh = 0.0;
@@ -695,18 +689,27 @@ __device__ __forceinline__ ZBounds z_bounds(const SliceHdr& hd, bool own, float 
       no_zf = 1;
     }
   }
-  lo = wsum_f64(lo);
-  hi = wsum_f64(hi);
-  zl = wsum_f64(zl);
-  zh = wsum_f64(zh);
-  const bool allzf = wsum_i(no_zf) == 0;
+  // lanes 0..G-1 hold the slices: read them directly
+  auto lane_f64 = [](double v, int l) {
+    return __longlong_as_double((long long)lane_u64((uint64_t)__double_as_longlong(v), l));
+  };
+  double slo = 0.0, shi = 0.0, szl = 0.0, szh = 0.0;
+  int nz = 0;
+#pragma unroll
+  for (int l = 0; l < G; ++l) {
+    slo += lane_f64(lo, l);
+    shi += lane_f64(hi, l);
+    szl += lane_f64(zl, l);
+    szh += lane_f64(zh, l);
+    nz += (int)lane_u32((uint32_t)no_zf, l);
+  }
   const double LIM = 4.0e18;
   ZBounds z;
-  z.lo = Scand + (uint64_t)fmax(lo, 0.0);
-  z.hi = (hi >= LIM) ? (1ull << 62) : Scand + (uint64_t)ceil(hi);
-  if (allzf) {
-    const uint64_t a = zl <= 0.0 ? 0ull : (uint64_t)zl;
-    const uint64_t c = zh >= LIM ? (1ull << 62) : (uint64_t)ceil(zh);
+  z.lo = Scand + (uint64_t)fmax(slo, 0.0);
+  z.hi = (shi >= LIM) ? (1ull << 62) : Scand + (uint64_t)ceil(shi);
+  if (nz == 0) {
+    const uint64_t a = szl <= 0.0 ? 0ull : (uint64_t)szl;
+    const uint64_t c = szh >= LIM ? (1ull << 62) : (uint64_t)ceil(szh);
     z.lo = a > z.lo ? a : z.lo;
     z.hi = c < z.hi ? c : z.hi;
   }
@@ -745,6 +748,9 @@ struct RegStore {
   int ci[QM];
   uint64_t w[QM];  // exp_fix44(l - m) (replaced by the draw weights at the end)
   uint32_t al;
+  // masses of the alive set (all / covered) while no filter has changed it
+  bool cached;
+  uint64_t m_all, m_cov;
 
   __device__ __forceinline__ bool on(int t) const { return (al >> t) & 1u; }
   template <typename F>
@@ -767,6 +773,7 @@ struct RegStore {
 #pragma unroll
     for (int t = 0; t < QM; ++t) m |= (on(t) && f(t)) ? (1u << t) : 0u;
     al = m;
+    cached = false;
   }
   // Smallest / largest key and id over alive slots where f holds (wave).
   template <typename F>
@@ -800,9 +807,13 @@ struct RegStore {
 
   __device__ __forceinline__ int count() const { return count_if([](int) { return true; }); }
   __device__ __forceinline__ uint64_t mass(bool cov_only, float tcov) const {
+    if (cached) return cov_only ? m_cov : m_all;
     return mass_if([&](int t) { return !cov_only || cl[t] >= tcov; });
   }
-  __device__ __forceinline__ void none() { al = 0; }
+  __device__ __forceinline__ void none() {
+    al = 0;
+    cached = false;
+  }
   __device__ __forceinline__ void keep_min(float thr) {
     keep_if([&](int t) { return cl[t] >= thr; });
   }
@@ -882,6 +893,7 @@ struct RegStore {
 struct MergeSmem {
   uint64_t hist[1024];
   uint64_t bc64[2];
+  uint64_t bucket[64];  // register merge: draw buckets
 };
 
 struct WaveCands {
@@ -1056,8 +1068,10 @@ __device__ __forceinline__ bool run_filters(St& st, const SampleKArgs& a, const 
 // Register merge of row b by wave 0.  `st` holds slots t < G (the first 64
 // candidates of slice t, loaded with the summaries); slots G..G*TS-1 are
 // loaded here.  Returns the path code (0 done, 3 exact engine).
+template <int G>
 __device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& P, int b, const RowParams& rp,
-                                          const SliceHdr& hd, int G, float m, float tcov, float ub, RegStore& st, int TS) {
+                                          const SliceHdr& hd, float m, float tcov, float ub, RegStore& st, int TS,
+                                          MergeSmem& sm) {
   const int lane = threadIdx.x & 63;
   const int hn = lane < G ? hd.n : 0;
   if (TS > 1) {
@@ -1085,8 +1099,20 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& 
   }
 #pragma unroll
   for (int t = 0; t < QM; ++t) st.w[t] = (t < G * TS && st.on(t)) ? exp_fix44(st.cl[t] - m) : 0ull;
-  const uint64_t Scand = st.mass(false, 0.0f);
-  const ZBounds zb = z_bounds(hd, lane < G, m, Scand);
+  {
+    uint64_t mv[2] = {0ull, 0ull};
+#pragma unroll
+    for (int t = 0; t < QM; ++t) {
+      mv[0] += st.w[t];
+      mv[1] += st.cl[t] >= tcov ? st.w[t] : 0ull;
+    }
+    wsum_u64_k<2>(mv);
+    st.m_all = mv[0];
+    st.m_cov = mv[1];
+    st.cached = true;
+  }
+  const uint64_t Scand = st.m_all;
+  const ZBounds zb = z_bounds<G>(hd, lane < G, m, Scand);
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
 
   // Draw: integer inverse CDF in vocabulary order over the kept slots.
@@ -1097,52 +1123,95 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& 
     for (int t = 0; t < QM; ++t)
       st.w[t] = (t < G * TS && st.on(t)) ? exp_fix44(chain_scale(a.chain, st.cl[t] - m, invT, Tc)) : 0ull;
   }
-  // Each slice's candidates are sorted by id and slot t holds chunk t / G of
-  // slice t % G, so vocabulary order is (slice, chunk, lane).  The slot
-  // totals in that order locate the slot holding the target; one prefix scan
-  // of that slot then gives the first kept element whose inclusive sum
-  // exceeds it.
-  const int GT = G * TS;
-  uint64_t tot[QM];
+  // Slot t holds chunk t / G of slice t % G and slices are vocabulary
+  // ranges in order, so the per-slice kept masses locate the slice holding
+  // the target.  Inside that slice the candidates are in no order: each kept
+  // one is broadcast in turn (an s_ff1 walk over the kept lanes of each of
+  // the slice's slots) and every lane adds its weight to its own elements'
+  // inclusive sums when its id is not larger.  The draw is the smallest id
+  // whose inclusive sum exceeds the target.
+  uint64_t st_tot[G];
 #pragma unroll
-  for (int t = 0; t < QM; ++t) tot[t] = t < GT ? wsum_u64(st.on(t) ? st.w[t] : 0ull) : 0ull;
+  for (int sl = 0; sl < G; ++sl) {
+    uint64_t v = 0;
+#pragma unroll
+    for (int t = sl; t < QM; t += G) v += (t < G * TS && st.on(t)) ? st.w[t] : 0ull;
+    st_tot[sl] = v;
+  }
+  wsum_u64_k<G>(st_tot);
   uint64_t ZV = 0;
 #pragma unroll
-  for (int t = 0; t < QM; ++t) ZV += tot[t];
+  for (int sl = 0; sl < G; ++sl) ZV += st_tot[sl];
   const int nkept = st.count();
   if (a.tokens) {
     int tok = 0;
     if (ZV) {
       const uint64_t tgt = draw_target(ub, ZV);
-      // walk the slots in (slice, chunk) order
-      uint64_t before = 0;
-      int ts = -1;
-      uint64_t rem = 0;
-      for (int sl = 0; sl < G && ts < 0; ++sl)
-        for (int ch = 0; ch < TS && ts < 0; ++ch) {
-          const int t = ch * G + sl;
-          uint64_t tt = 0;
+      uint64_t before = 0, rem = 0;
+      int ss = -1;
 #pragma unroll
-          for (int u2 = 0; u2 < QM; ++u2) tt = u2 == t ? tot[u2] : tt;
-          if (before + tt > tgt) {
-            ts = t;
-            rem = tgt - before;
+      for (int sl = 0; sl < G; ++sl) {
+        if (ss < 0 && before + st_tot[sl] > tgt) {
+          ss = sl;
+          rem = tgt - before;
+        }
+        before += st_tot[sl];
+      }
+      // bucket the slice's kept weights by id (64 buckets of 2^sh ids), find
+      // the bucket holding the target with one prefix scan, then walk only
+      // that bucket's kept candidates
+      int sh = 0;
+      while (((P.SL - 1) >> sh) >= 64) ++sh;
+      const int v0s = ss * P.SL;
+      sm.bucket[lane] = 0;
+      wave_sync();
+#pragma unroll
+      for (int sl = 0; sl < G; ++sl) {
+        if (sl != ss) continue;
+#pragma unroll
+        for (int c = 0; c < QM / G; ++c) {
+          const int t = c * G + sl;
+          if (c < TS && st.on(t)) atomicAdd((unsigned long long*)&sm.bucket[(st.ci[t] - v0s) >> sh], (unsigned long long)st.w[t]);
+        }
+      }
+      wave_sync();
+      const uint64_t bv = sm.bucket[lane];
+      const uint64_t incl = wscan_u64(bv);
+      const uint64_t hitb = __ballot(incl > rem);
+      const int bsel = (int)__ffsll((long long)hitb) - 1;
+      const uint64_t rem2 = rem - (lane_u64(incl, bsel) - lane_u64(bv, bsel));
+      uint64_t cum[QM / G];
+#pragma unroll
+      for (int c = 0; c < QM / G; ++c) cum[c] = 0;
+#pragma unroll
+      for (int sl = 0; sl < G; ++sl) {
+        if (sl != ss) continue;
+        auto inb = [&](int t) { return st.on(t) && ((st.ci[t] - v0s) >> sh) == bsel; };
+#pragma unroll
+        for (int c = 0; c < QM / G; ++c) {
+          const int t = c * G + sl;
+          if (c >= TS) break;
+          uint64_t kept = __ballot(inb(t));
+          while (kept) {
+            const int j = (int)__ffsll((long long)kept) - 1;
+            kept &= kept - 1;
+            const uint32_t idj = lane_u32((uint32_t)st.ci[t], j);
+            const uint64_t wj = lane_u64(st.w[t], j);
+#pragma unroll
+            for (int c2 = 0; c2 < QM / G; ++c2) {
+              const int t2 = c2 * G + sl;
+              cum[c2] += (c2 < TS && (uint32_t)st.ci[t2] >= idj) ? wj : 0ull;
+            }
           }
-          before += tt;
         }
-      uint64_t wv = 0;
-      int iv = 0;
-      bool ov = false;
+        int best = 0x7FFFFFFF;
 #pragma unroll
-      for (int t = 0; t < QM; ++t)
-        if (t == ts) {
-          wv = st.on(t) ? st.w[t] : 0ull;
-          iv = st.ci[t];
-          ov = st.on(t);
+        for (int c = 0; c < QM / G; ++c) {
+          const int t = c * G + sl;
+          if (c < TS && inb(t) && cum[c] > rem2) best = min(best, st.ci[t]);
         }
-      const uint64_t incl = wscan_u64(wv);
-      const uint64_t hit = __ballot(ov && incl > rem);
-      if (hit) tok = (int)lane_u32((uint32_t)iv, (int)__ffsll((long long)hit) - 1);
+        tok = wmin_i(best);
+      }
     }
     if (lane == 0) a.tokens[b] = tok;
   }
@@ -1199,7 +1268,17 @@ __device__ __noinline__ int merge_lds(const SampleKArgs* ap, const FastPlan* pp,
   st.m = m;
   st.sm = &sm;
   const uint64_t Scand = st.mass(false, 0.0f);
-  const ZBounds zb = z_bounds(hd, lane < G, m, Scand);
+  ZBounds zb;
+  switch (G) {
+    case 1: zb = z_bounds<1>(hd, lane < G, m, Scand); break;
+    case 2: zb = z_bounds<2>(hd, lane < G, m, Scand); break;
+    case 3: zb = z_bounds<3>(hd, lane < G, m, Scand); break;
+    case 4: zb = z_bounds<4>(hd, lane < G, m, Scand); break;
+    case 5: zb = z_bounds<5>(hd, lane < G, m, Scand); break;
+    case 6: zb = z_bounds<6>(hd, lane < G, m, Scand); break;
+    case 7: zb = z_bounds<7>(hd, lane < G, m, Scand); break;
+    default: zb = z_bounds<8>(hd, lane < G, m, Scand); break;
+  }
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
   const float invT = (float)(1.0 / (double)rp.T);
   const float Tc = (float)fmax((double)rp.T, 1e-5);
@@ -1234,6 +1313,7 @@ __device__ __noinline__ int merge_lds(const SampleKArgs* ap, const FastPlan* pp,
 }
 
 
+template <int G>
 __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ ExactSmem esm;
@@ -1241,7 +1321,6 @@ __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
   __shared__ int s_path;
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
-  const int G = P.G;
   const RowRaw raw = row_raw(a, b);
   const RowParams rp = row_params(a, raw, P.rule_cap);
   if (tid < 64) {
@@ -1253,6 +1332,7 @@ __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
     const SliceHdr hd = P.hdr[(long long)b * G + min(lane, G - 1)];
     const float ub = (a.tokens && !rp.greedy) ? a.u[b] : 0.0f;
     RegStore st;
+    st.cached = false;
 #pragma unroll
     for (int t = 0; t < QM; ++t) {
       int2 c = make_int2(0, -1);
@@ -1263,9 +1343,17 @@ __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
     // compiler barrier: keep every load above issued here, before anything
     // waits on the summaries (no hardware wait is implied)
     asm volatile("" ::: "memory");
-    const float m = wmax_f(lane < G ? hd.m : -INFINITY);
-    const int flagged = wsum_i(lane < G ? (hd.flags & HDR_OVERFLOW) : 0);
-    const int unsorted = wsum_i(lane < G ? (hd.flags & HDR_UNSORTED) : 0);
+    // the G summaries sit in lanes 0..G-1: aggregate them with readlanes
+    float m = -INFINITY, tcov = -INFINITY;
+    int fl = 0, nmax = 0;
+#pragma unroll
+    for (int l = 0; l < G; ++l) {
+      m = fmaxf(m, __uint_as_float(lane_u32(__float_as_uint(hd.m), l)));
+      tcov = fmaxf(tcov, __uint_as_float(lane_u32(__float_as_uint(hd.tau), l)));
+      fl |= (int)lane_u32((uint32_t)hd.flags, l);
+      nmax = max(nmax, (int)lane_u32((uint32_t)hd.n, l));
+    }
+    const int flagged = fl & HDR_OVERFLOW;
     int path;
     if (rp.greedy) {
       const int bi = wmin_i((lane < G && hd.m == m) ? hd.best_i : 0x7FFFFFFF);
@@ -1281,10 +1369,8 @@ __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
     } else if (flagged || rp.all) {
       path = 1;
     } else {
-      const float tcov = wmax_f(lane < G ? hd.tau : -INFINITY);
-      const int nmax = wmax_i(lane < G ? hd.n : 0);
       const int TS = (nmax + 63) / 64;
-      if (G * TS <= QM && G <= QSPEC && !unsorted) path = merge_regs(a, P, b, rp, hd, G, m, tcov, ub, st, TS);
+      if (G * TS <= QM && G <= QSPEC) path = merge_regs<G>(a, P, b, rp, hd, m, tcov, ub, st, TS, sm);
       else path = merge_lds(&kernargs()->a, &kernargs()->p, b, rp, G, m, tcov, ub, dyn, &sm);
     }
     if (lane == 0) {
@@ -1384,6 +1470,29 @@ static int launch_slice(int dtype, int R, const SampleKArgs& k, const FastPlan& 
   return launch_slice_t<0, 12>(k, fp, lds, st);
 }
 
+template <int G>
+static int launch_merge_t(const SampleKArgs& k, const FastPlan& fp, size_t lds, hipStream_t st) {
+  auto fn = merge_kernel<G>;
+  int rc = set_lds((const void*)fn, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(fn, dim3(k.B), dim3(512), lds, st, k, fp);
+  return WH_OK;
+}
+
+// The merge is compiled per slice count (slot -> slice / chunk maps are then
+// constants); plans use 1..6 slices.
+static int launch_merge(const SampleKArgs& k, const FastPlan& fp, size_t lds, hipStream_t st) {
+  switch (fp.G) {
+    case 1: return launch_merge_t<1>(k, fp, lds, st);
+    case 2: return launch_merge_t<2>(k, fp, lds, st);
+    case 3: return launch_merge_t<3>(k, fp, lds, st);
+    case 4: return launch_merge_t<4>(k, fp, lds, st);
+    case 5: return launch_merge_t<5>(k, fp, lds, st);
+    case 6: return launch_merge_t<6>(k, fp, lds, st);
+    default: return fail(WH_EINVAL, "no merge kernel for %d slices", fp.G);
+  }
+}
+
 int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st) {
   const int esz = k0.dtype == WH_DTYPE_BF16 ? 2 : 4;
   HostPlan hp = make_plan(k0.B, k0.V, k0.dtype, k0.hcap);
@@ -1408,9 +1517,8 @@ int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st
   if (rc) return rc;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "slice_kernel launch failed: %s", hipGetErrorString(e));
-  rc = set_lds((const void*)merge_kernel, lds_merge);
+  rc = launch_merge(k, fp, lds_merge, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(merge_kernel, dim3(k.B), dim3(512), lds_merge, st, k, fp);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "merge_kernel launch failed: %s", hipGetErrorString(e));
   return WH_OK;
