@@ -94,6 +94,20 @@ def make_sets(w, nsets, dev):
     return sets
 
 
+def measured_traffic(workload: int, name: str):
+    """HBM bytes per call from the committed rocprofv3 --pmc summary of this
+    workload (FETCH_SIZE and WRITE_SIZE runs, each scaled by what the counter
+    reads for a 256 MiB copy), or None when there is none for this workload."""
+    path = os.path.join(ROOT, "profiles", f"wh_sample_workload{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        t = json.load(f)
+    if t.get("workload") != name:
+        return None, None
+    return int(t["traffic_bytes_per_call"]), t.get("source")
+
+
 def cpu_baseline(w, seconds: float):
     from oracle import oracle as o
     from whallm_amd import synth
@@ -176,6 +190,7 @@ def main():
     parity["timed_set0_tokens_bit_exact"] = bool(np.array_equal(tok_set0, want))
     nbytes = w.bytes_per_call()
     achieved = nbytes / avg_s / 1e9
+    traffic, traffic_src = measured_traffic(args.workload, w.name)
     res = {
         "metric": METRIC,
         "value": w.B * args.steps / wall,
@@ -193,9 +208,10 @@ def main():
                    "history": None if w.history is None else int(w.history.shape[1]),
                    "input_sets": len(sets), "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "kernel": "wh_sample (slice_kernel + merge_kernel)",
-                     "kernel_avg_us": avg_s * 1e6, "algorithmic_bytes": nbytes},
+                     "kernel_avg_us": avg_s * 1e6, "algorithmic_bytes": nbytes,
+                     "traffic_source": traffic_src},
         "parity": parity,
     }
     if not args.no_cpu_baseline:

@@ -365,12 +365,20 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   // for exactly the loads it needs.
   const int32_t* hrow = a.hist + (long long)b * a.hist_stride;
   if (pen) {
-    len = max(0, min(*(cint*)(a.hist_len + b), hs));
-    // rows longer than the prefetch read the last HPF * FT positions (every
-    // window is a suffix of at most WH_MAX_WINDOW ids)
-    if (!pf) jbase = max(0, len - HPF * FT);
+    if (pf) {
+      // the addresses do not wait for the length (a scalar load still in
+      // flight while the logits loads issue)
 #pragma unroll
-    for (int q = 0; q < HPF; ++q) hreg[q] = hrow[min(jbase + tid + q * FT, hs - 1)];
+      for (int q = 0; q < HPF; ++q) hreg[q] = hrow[min(tid + q * FT, hs - 1)];
+      len = max(0, min(*(cint*)(a.hist_len + b), hs));
+    } else {
+      // rows longer than the prefetch read the last HPF * FT positions
+      // (every window is a suffix of at most WH_MAX_WINDOW ids)
+      len = max(0, min(*(cint*)(a.hist_len + b), hs));
+      jbase = max(0, len - HPF * FT);
+#pragma unroll
+      for (int q = 0; q < HPF; ++q) hreg[q] = hrow[min(jbase + tid + q * FT, hs - 1)];
+    }
   }
   const char* rowp = (const char*)a.logits + (size_t)b * a.row_stride * ESZ;
   uint4 d[R];
