@@ -22,11 +22,13 @@ typedef unsigned __int128 u128;
 // for this library; float32 Horner error <= 0.55 ulp).  Inputs d <= 0;
 // t <= -45 and -inf give 0.
 // --------------------------------------------------------------------------
+// Written without branches (the flushed case computes on t = 0 and is
+// selected away), so wave code over many slots stays straight-line.
 __device__ __forceinline__ uint64_t exp_fix44(float d) {
   const float L = 0x1.715476p+0f;
   float t = d * L;
-  if (!(t > -45.0f)) return 0;
-  if (t > 0.0f) t = 0.0f;
+  const bool flush = !(t > -45.0f);
+  t = (flush || t > 0.0f) ? 0.0f : t;
   float n = floorf(t);
   float f = t - n;
   float p = 0x1.c5417ap-13f;
@@ -38,7 +40,8 @@ __device__ __forceinline__ uint64_t exp_fix44(float d) {
   p = fmaf(p, f, 1.0f);
   uint32_t mant = (uint32_t)(p * 8388608.0f);
   int sh = (int)n + 21;
-  return sh >= 0 ? ((uint64_t)mant << sh) : (uint64_t)(mant >> (-sh));
+  const uint64_t r = sh >= 0 ? ((uint64_t)mant << sh) : (uint64_t)(mant >> (-sh));
+  return flush ? 0ull : r;
 }
 
 // float32 mantissa/exponent split: x = M * 2^(e - 24), M a 24-bit integer.
@@ -201,6 +204,41 @@ __device__ __forceinline__ void wsum_u64_k(uint64_t (&v)[K]) {
 #undef WH_DPPK_STEP
 #pragma unroll
   for (int k = 0; k < K; ++k) v[k] = (lane_u64(v[k], 0) + lane_u64(v[k], 16)) + (lane_u64(v[k], 32) + lane_u64(v[k], 48));
+}
+
+// Inclusive prefix sum over the 64 lanes (lane order), all lanes active.
+// Hillis-Steele inside each row of 16 (row_shr 1, 2, 4, 8), then
+// row_bcast:15 carries row 0 into row 1 and row 2 into row 3, and
+// row_bcast:31 carries rows 0-1 into rows 2-3.  Lanes a step does not
+// write (no source lane, or a row outside its row mask) add 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp32z(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROWS, 0xF, true);
+}
+__device__ __forceinline__ uint64_t wscan_incl_u64(uint64_t x) {
+#define WH_SCAN_STEP(C, ROWS)                                                                                \
+  {                                                                                                           \
+    const uint64_t y_ = ((uint64_t)dpp32z<C, ROWS>((uint32_t)(x >> 32)) << 32) | dpp32z<C, ROWS>((uint32_t)x); \
+    x += y_;                                                                                                  \
+  }
+  WH_SCAN_STEP(0x111, 0xF)
+  WH_SCAN_STEP(0x112, 0xF)
+  WH_SCAN_STEP(0x114, 0xF)
+  WH_SCAN_STEP(0x118, 0xF)
+  WH_SCAN_STEP(0x142, 0xA)
+  WH_SCAN_STEP(0x143, 0xC)
+#undef WH_SCAN_STEP
+  return x;
+}
+
+__device__ __forceinline__ uint32_t wscan_incl_u32(uint32_t x) {
+  x += dpp32z<0x111, 0xF>(x);
+  x += dpp32z<0x112, 0xF>(x);
+  x += dpp32z<0x114, 0xF>(x);
+  x += dpp32z<0x118, 0xF>(x);
+  x += dpp32z<0x142, 0xA>(x);
+  x += dpp32z<0x143, 0xC>(x);
+  return x;
 }
 
 // Number of lanes (of the active ones) where p holds; wave uniform.

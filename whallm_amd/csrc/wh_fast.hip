@@ -35,11 +35,12 @@
 //     sum over the slice.
 //
 // merge_kernel: one workgroup per row.  Wave 0 loads the G summaries and the
-// first 64 candidates of every slice in one round trip.  It keeps up to eight
-// candidates per lane in registers and runs the integer contract over them:
+// first QSPEC 64-candidate chunks of the row (chunk t / G of slice t % G) in
+// one round trip.  It keeps up to 16 candidates per lane in registers and runs
+// the integer contract over them:
 //   * the proven interval [Zlo, Zhi] for the normaliser;
 //   * top-k / top-p / min-p in the chain's order;
-//   * the inverse-CDF draw.
+//   * the inverse-CDF draw, a 6-bit radix descent over the id.
 // Cut points are found by bitwise searches over value/id composites, with
 // ballot counts and DPP sums.  Larger candidate sets go through LDS with a
 // radix select.  The exact engine finishes a row the candidates cannot
@@ -50,15 +51,16 @@
 
 namespace wh {
 
-constexpr int FT = 1024;          // slice-kernel threads per workgroup
+constexpr int FT = 1024;          // slice-kernel threads per workgroup (four waves per SIMD)
 constexpr int FNW = FT / 64;      // waves per slice workgroup
 constexpr int FAST_NE = 48;       // logits per thread held in VGPRs, at most
 constexpr int GPREF = 4;          // slices per row preferred for small batches
+constexpr int GMAX = 6;           // slices per row the merge is compiled for
 constexpr int FAST_CAP = 2048;    // candidate capacity per slice
 constexpr int RUNGS = 8;          // thresholds per ladder round
 constexpr int LADDER_ROUNDS = 4;  // ladder rounds at most (the first plus refinements)
-constexpr int QM = 16;            // merge: candidate slots per lane
-constexpr int QSPEC = 8;          // merge: slots loaded speculatively with the summaries (slices <= 8)
+constexpr int QM = 16;            // merge: candidate slots per lane, at most
+constexpr int QSPEC = 16;         // merge: slots loaded speculatively with the summaries (slices <= 16)
 constexpr int HDR_OVERFLOW = 1;   // SliceHdr.flags: the row needs the exact engine
 constexpr float BAND1 = 1.5f;     // band floors below tau, nats
 constexpr float BAND2 = 3.5f;
@@ -84,7 +86,6 @@ struct FastPlan {
   int rule_cap;    // largest k a slice may bound
   int pcap;        // capacity of the penalised-element list (with penalties)
   int codes_bytes; // LDS bytes of the penalty codes (0 without penalties)
-  int cand_off;    // LDS offset of the candidate buffer
   int* path;       // [B] 0: merged in registers, 4: merged through LDS, 1: exact engine
                    //     (overflow / no bound), 2: greedy, 3: exact engine (top-p cut unsettled)
   SliceHdr* hdr;   // [B * G]
@@ -216,7 +217,7 @@ struct SliceSmem {
   float redm[FNW];
   int redg[FNW];
   int lad[LADDER_ROUNDS][RUNGS];  // ladder totals per round (zeroed at kernel start)
-  int redb[FNW][2];
+  int redb[FNW][1];
   double redz[FNW];
 };
 
@@ -353,7 +354,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   //    first wait.
   const RowRaw raw = row_raw(a, b);
   const bool pen = a.hcap > 0;
-  constexpr int HPF = 4;  // history positions per thread: HPF * FT >= WH_MAX_WINDOW
+  constexpr int HPF = WH_MAX_WINDOW / FT;  // history positions per thread
   const int hs = (int)a.hist_stride;
   const bool pf = hs <= HPF * FT;  // the whole history row fits the prefetch
   int hreg[HPF];
@@ -369,7 +370,8 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
       // the addresses do not wait for the length (a scalar load still in
       // flight while the logits loads issue)
 #pragma unroll
-      for (int q = 0; q < HPF; ++q) hreg[q] = hrow[min(tid + q * FT, hs - 1)];
+      for (int q = 0; q < HPF; ++q)
+        if (q * FT < hs) hreg[q] = hrow[min(tid + q * FT, hs - 1)];
       len = max(0, min(*(cint*)(a.hist_len + b), hs));
     } else {
       // rows longer than the prefetch read the last HPF * FT positions
@@ -401,22 +403,27 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     sm.npatch = 0;
   }
 
-  // 2. penalties, from the history side.  Each in-window id of this slice is
-  //    entered in a dense u16 code per slice element (count in the frequency
-  //    window, repetition / presence flags); the thread whose atomic first
-  //    touches an element owns it.  Owners turn their element's final code and
-  //    raw logit (a gather from the row, issued as soon as the ids arrive) into
-  //    the penalised value, list it, and set the code to 0xFFFF.  The threads
-  //    holding the logits then OR the codes into their registers: a penalised
-  //    element becomes NaN there, which every max and >= test ignores, and it
-  //    lives on only in the list.
-  uint32_t* codes = (uint32_t*)dyn;
-  uint16_t* codes16 = (uint16_t*)dyn;
+  // 2. penalties, from the history side, and 3. the group maxima.
+  //    Each slice element has an element-sized code in LDS (u16 for bf16,
+  //    u32 for float32): the count in the frequency window (bits 0-12) and
+  //    the repetition / presence flags.  The in-window history ids of this
+  //    slice enter it with LDS atomics; the thread whose atomic first touches
+  //    an element owns it.  All of this needs only the history, so it runs
+  //    while the logits are still in flight.  Owners then keep the final code
+  //    and mark the element with all-ones.  As each 16-byte group lands, its
+  //    holder ANDs the codes into a copy (the raw bits of marked elements),
+  //    writes that back into the code slots, and ORs the codes into the
+  //    registers: a penalised element becomes a NaN there, which every max
+  //    and >= test ignores.  After one more barrier the owners read the raw
+  //    bits, apply the penalties and list the element, which lives on only in
+  //    the list.
+  char* codes = dyn;
   int2* patch = (int2*)(dyn + P.codes_bytes);
-  int2* cbuf = (int2*)(dyn + P.cand_off);
   float pmax = -INFINITY;
+  PenCtx pc;
+  uint32_t own = 0;
+  uint32_t ocode[HPF];
   if (pen) {
-    PenCtx pc;
     pc.rep = a.rep;
     pc.pres = a.pres;
     pc.freq = a.freq;
@@ -433,31 +440,28 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     const int words = P.codes_bytes / 16;
     for (int w = tid; w < words; w += FT) ((uint4*)codes)[w] = make_uint4(0u, 0u, 0u, 0u);
     bool inw[HPF];
-    uint32_t rawv[HPF];
 #pragma unroll
     for (int q = 0; q < HPF; ++q) {
       const int j = jbase + tid + q * FT;
       const int t = hreg[q];
       inw[q] = j >= len - W && j < len && t >= v0 && t < v1;
-      const int tc = min(max(t, v0), v1 - 1);
-      rawv[q] = DT ? (uint32_t)*(const uint16_t*)(rowp + (size_t)tc * 2) : *(const uint32_t*)(rowp + (size_t)tc * 4);
     }
     __syncthreads();
-    uint32_t own = 0;
 #pragma unroll
     for (int q = 0; q < HPF; ++q) {
       if (!inw[q]) continue;
       const int j = jbase + tid + q * FT;
-      const int o = hreg[q] - v0;
-      const int sh = (o & 1) * 16;
+      const int ob = (hreg[q] - v0) * ESZ;  // byte offset of the element's code
+      uint32_t* word = (uint32_t*)(codes + (ob & ~3));
+      const int sh = (ob & 3) * 8;
       const uint32_t add = (pc.on_f && j >= len - wf) ? 1u : 0u;
       const uint32_t fl = ((pc.on_r && !pc.dr && j >= len - wr) ? PEN_R : 0u) | ((pc.on_p && !pc.dp && j >= len - wp) ? PEN_P : 0u);
       // the first read-modify-write of the element's code sees 0 (every
       // update leaves it non-zero): that thread owns the element
       uint32_t old = 0xFFFFFFFFu;
-      if (add) old = atomicAdd(&codes[o >> 1], add << sh);
+      if (add) old = atomicAdd(word, add << sh);
       if (fl) {
-        const uint32_t o2 = atomicOr(&codes[o >> 1], fl << sh);
+        const uint32_t o2 = atomicOr(word, fl << sh);
         if (!add) old = o2;
       }
       if (((old >> sh) & 0xFFFFu) == 0u) own |= 1u << q;
@@ -465,51 +469,56 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < HPF; ++q) {
+      ocode[q] = 0;
       if (!((own >> q) & 1u)) continue;
-      const int t = hreg[q];
-      const uint32_t code = codes16[t - v0];
-      const float l = (DT ? __uint_as_float(rawv[q] << 16) : __uint_as_float(rawv[q])) + 0.0f;
-      const float v = pc.apply(l, code);
-      const int slot = atomicAdd(&sm.npatch, 1);
-      if (slot < P.pcap) patch[slot] = make_int2(__float_as_int(v), t);
-      codes16[t - v0] = 0xFFFFu;
-      pmax = fmaxf(pmax, v);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int g = v0 + (r * FT + tid) * EPT;
-      if (g < v1) {
-        const char* cp = (const char*)codes + (size_t)(g - v0) * 2;
-        if (DT) {
-          const uint4 cw = *(const uint4*)cp;
-          d[r].x |= cw.x;
-          d[r].y |= cw.y;
-          d[r].z |= cw.z;
-          d[r].w |= cw.w;
-        } else {
-          const uint2 cw = *(const uint2*)cp;
-          d[r].x |= (cw.x & 0xFFFFu) * 0x10001u;
-          d[r].y |= (cw.x >> 16) * 0x10001u;
-          d[r].z |= (cw.y & 0xFFFFu) * 0x10001u;
-          d[r].w |= (cw.y >> 16) * 0x10001u;
-        }
+      const int o = hreg[q] - v0;
+      if (DT) {
+        ocode[q] = ((uint16_t*)codes)[o];
+        ((uint16_t*)codes)[o] = 0xFFFFu;
+      } else {
+        ocode[q] = ((uint32_t*)codes)[o];
+        ((uint32_t*)codes)[o] = 0xFFFFFFFFu;
       }
     }
+    __syncthreads();
   }
-
-  // 3. group maxima and the slice max (one block reduction); padding groups
-  //    (duplicate loads) become -inf here
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-    if (v0 + (r * FT + tid) * EPT >= v1) d[r] = make_uint4(NEG, NEG, NEG, NEG);
+  // group maxima as the groups land (padding groups, duplicate loads, become
+  // -inf); with penalties, the marked elements are swapped out first
   float gm[R];
-  float mx = pmax;
+  float mx = -INFINITY;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
+    const int g = v0 + (r * FT + tid) * EPT;
+    if (pen && g < v1) {
+      uint4* cp = (uint4*)(codes + (size_t)(g - v0) * ESZ);
+      const uint4 cw = *cp;
+      if ((cw.x | cw.y | cw.z | cw.w) != 0u) {
+        *cp = make_uint4(d[r].x & cw.x, d[r].y & cw.y, d[r].z & cw.z, d[r].w & cw.w);
+        d[r].x |= cw.x;
+        d[r].y |= cw.y;
+        d[r].z |= cw.z;
+        d[r].w |= cw.w;
+      }
+    }
+    if (g >= v1) d[r] = make_uint4(NEG, NEG, NEG, NEG);
     gm[r] = grp_max<DT>(d[r]);
     mx = fmaxf(mx, gm[r]);
   }
+  if (pen) {
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < HPF; ++q) {
+      if (!((own >> q) & 1u)) continue;
+      const int t = hreg[q];
+      const float l = (DT ? __uint_as_float((uint32_t)((uint16_t*)codes)[t - v0] << 16)
+                          : __uint_as_float(((uint32_t*)codes)[t - v0])) + 0.0f;
+      const float v = pc.apply(l, ocode[q]);
+      const int slot = atomicAdd(&sm.npatch, 1);
+      if (slot < P.pcap) patch[slot] = make_int2(__float_as_int(v), t);
+      pmax = fmaxf(pmax, v);
+    }
+  }
+  mx = fmaxf(mx, pmax);
   mx = wmax_f(mx);
   if (lane == 0) sm.redm[wv] = mx;
   __syncthreads();
@@ -569,59 +578,83 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   const float t1 = tau - BAND1, t2 = tau - BAND2;
   const bool need_zf = rp.use_p && !rp.tm;
 
-  // 5. candidates from the groups whose max reaches tau; group band counts;
-  //    optional hardware-exp sum
-  int n1 = 0, n2 = 0;
+  // 5. candidates from the groups whose max reaches tau, written straight to
+  //    the workspace; group band counts; optional hardware-exp sum
+  int2* gc = P.cand + ((long long)b * P.G + s) * P.cap;
+  // groups (and listed penalised elements) at or above tau, t1 and t2; the
+  // band counts are the differences (a NaN group max counts nowhere)
+  int c0 = 0, c1 = 0, c2 = 0;
   float zs = 0.0f;
+  // element masks of the candidate groups, 8 bits per group
+  uint32_t mk[(R + 3) / 4];
+#pragma unroll
+  for (int q = 0; q < (R + 3) / 4; ++q) mk[q] = 0u;
+  int tcnt = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const float x = gm[r];
-    n1 += (x >= t1 && !(x >= tau)) ? 1 : 0;
-    n2 += (x >= t2 && !(x >= t1)) ? 1 : 0;
+    c0 += x >= tau ? 1 : 0;
+    c1 += x >= t1 ? 1 : 0;
+    c2 += x >= t2 ? 1 : 0;
     const int g = v0 + (r * FT + tid) * EPT;
-    if (x >= tau && g < v1) {
-      // one LDS atomic reserves the group's slots (penalised elements are NaN
-      // here and fail the test; a group lies wholly inside or outside the slice)
+    const bool cg = x >= tau && g < v1;
+    if (__ballot(cg)) {
+      // penalised elements are NaN here and fail the test; a group lies
+      // wholly inside or outside the slice
       uint32_t msk = 0;
 #pragma unroll
       for (int e = 0; e < EPT; ++e) msk |= (elem<DT>(d[r], e) >= tau) ? (1u << e) : 0u;
-      int slot = atomicAdd(&sm.cnt, (int)__popc(msk));
-#pragma unroll
-      for (int e = 0; e < EPT; ++e) {
-        if ((msk >> e) & 1u) {
-          if (slot < P.cap) cbuf[slot] = make_int2(__float_as_int(elem_n<DT>(d[r], e)), g + e);
-          ++slot;
-        }
-      }
+      msk = cg ? msk : 0u;
+      mk[r >> 2] |= msk << (8 * (r & 3));
+      tcnt += __popc(msk);
     }
     if (need_zf) {
 #pragma unroll
       for (int e = 0; e < EPT; ++e) zs += __expf(fmaxf(elem<DT>(d[r], e), -INFINITY) - ms);  // NaN (penalised) -> 0
     }
   }
+  if (__ballot(tcnt > 0)) {
+    // The wave reserves its slots with one LDS atomic: an inclusive scan of
+    // the per-lane counts gives each lane its offset.
+    const uint32_t incl = wscan_incl_u32((uint32_t)tcnt);
+    int base = 0;
+    if (lane == 63) base = atomicAdd(&sm.cnt, (int)incl);
+    int slot = (int)lane_u32((uint32_t)base, 63) + (int)incl - tcnt;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      uint32_t msk = (mk[r >> 2] >> (8 * (r & 3))) & 0xFFu;
+      if (__ballot(msk != 0u)) {
+        const int g = v0 + (r * FT + tid) * EPT;
+        while (msk) {
+          const int e = __ffs(msk) - 1;
+          msk &= msk - 1u;
+          if (slot < P.cap) gc[slot] = make_int2(__float_as_int(elem_n<DT>(d[r], e)), g + e);
+          ++slot;
+        }
+      }
+    }
+  }
   for (int p = tid; p < npatch; p += FT) {
     const float v = __int_as_float(patch[p].x);
-    n1 += (v >= t1 && !(v >= tau)) ? 1 : 0;
-    n2 += (v >= t2 && !(v >= t1)) ? 1 : 0;
+    c0 += v >= tau ? 1 : 0;
+    c1 += v >= t1 ? 1 : 0;
+    c2 += v >= t2 ? 1 : 0;
     if (v >= tau) {
       const int slot = atomicAdd(&sm.cnt, 1);
-      if (slot < P.cap) cbuf[slot] = make_int2(patch[p].x, patch[p].y);
+      if (slot < P.cap) gc[slot] = make_int2(patch[p].x, patch[p].y);
     }
     if (need_zf) zs += __expf(v - ms);
   }
-  n1 = wsum_i(n1);
-  n2 = wsum_i(n2);
+  // n1 | n2 << 16 in one reduction (at most 7 per thread, 7168 per slice)
+  const int pk = wsum_i((c1 - c0) | ((c2 - c1) << 16));
   const double zw = need_zf ? wsum_f64((double)zs) : 0.0;
   if (lane == 0) {
-    sm.redb[wv][0] = n1;
-    sm.redb[wv][1] = n2;
+    sm.redb[wv][0] = pk;
     sm.redz[wv] = zw;
   }
   __syncthreads();
   const int n = sm.cnt;
   const int nw = min(n, P.cap);
-  int2* gc = P.cand + ((long long)b * P.G + s) * P.cap;
-  for (int j = tid; j < nw; j += FT) gc[j] = cbuf[j];
   if (out) {
     // non-candidates are never kept; the merge writes the kept ones
 #pragma unroll
@@ -636,8 +669,8 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   if (wv == 0) {
     // lanes 0..15 read one wave's partials each; DPP sums finish them
     const bool lw = lane < FNW;
-    const int s1 = wsum_i(lw ? sm.redb[lane & (FNW - 1)][0] : 0);
-    const int s2 = wsum_i(lw ? sm.redb[lane & (FNW - 1)][1] : 0);
+    const int s12 = wsum_i(lw ? sm.redb[lane & (FNW - 1)][0] : 0);
+    const int s1 = s12 & 0xFFFF, s2 = s12 >> 16;
     const double sz = need_zf ? wsum_f64(lw ? sm.redz[lane & (FNW - 1)] : 0.0) : 0.0;
     if (lane == 0) {
     hdr->m = ms;
@@ -750,11 +783,13 @@ __device__ __forceinline__ uint64_t wscan_u64(uint64_t x) {
   return x;
 }
 
-// Candidates in registers: QM slots per lane, alive bits in `al`.
+// Candidates in registers: NS slots per lane (a compile-time count, so every
+// loop over the slots is straight-line code), alive bits in `al`.
+template <int NS>
 struct RegStore {
-  float cl[QM];
-  int ci[QM];
-  uint64_t w[QM];  // exp_fix44(l - m) (replaced by the draw weights at the end)
+  float cl[NS];
+  int ci[NS];
+  uint64_t w[NS];  // exp_fix44(l - m) (replaced by the draw weights at the end)
   uint32_t al;
   // masses of the alive set (all / covered) while no filter has changed it
   bool cached;
@@ -765,21 +800,21 @@ struct RegStore {
   __device__ __forceinline__ int count_if(F f) const {
     int c = 0;
 #pragma unroll
-    for (int t = 0; t < QM; ++t) c += ballot_count(on(t) && f(t));
+    for (int t = 0; t < NS; ++t) c += ballot_count(on(t) && f(t));
     return c;
   }
   template <typename F>
   __device__ __forceinline__ uint64_t mass_if(F f) const {
     uint64_t z = 0;
 #pragma unroll
-    for (int t = 0; t < QM; ++t) z += (on(t) && f(t)) ? w[t] : 0ull;
+    for (int t = 0; t < NS; ++t) z += (on(t) && f(t)) ? w[t] : 0ull;
     return wsum_u64(z);
   }
   template <typename F>
   __device__ __forceinline__ void keep_if(F f) {
     uint32_t m = 0;
 #pragma unroll
-    for (int t = 0; t < QM; ++t) m |= (on(t) && f(t)) ? (1u << t) : 0u;
+    for (int t = 0; t < NS; ++t) m |= (on(t) && f(t)) ? (1u << t) : 0u;
     al = m;
     cached = false;
   }
@@ -789,7 +824,7 @@ struct RegStore {
     kmn = 0xFFFFFFFFu;
     kmx = 0u;
 #pragma unroll
-    for (int t = 0; t < QM; ++t) {
+    for (int t = 0; t < NS; ++t) {
       const uint32_t k = fkey(cl[t]);
       const bool p = on(t) && f(t);
       kmn = p && k < kmn ? k : kmn;
@@ -803,7 +838,7 @@ struct RegStore {
     imn = 0xFFFFFFFFu;
     imx = 0u;
 #pragma unroll
-    for (int t = 0; t < QM; ++t) {
+    for (int t = 0; t < NS; ++t) {
       const uint32_t i = (uint32_t)ci[t];
       const bool p = on(t) && f(t);
       imn = p && i < imn ? i : imn;
@@ -901,7 +936,7 @@ struct RegStore {
 struct MergeSmem {
   uint64_t hist[1024];
   uint64_t bc64[2];
-  uint64_t bucket[64];  // register merge: draw buckets
+  uint64_t bucket[3][64];  // register merge: draw buckets, one array per radix level
 };
 
 struct WaveCands {
@@ -1073,53 +1108,44 @@ __device__ __forceinline__ bool run_filters(St& st, const SampleKArgs& a, const 
   return true;
 }
 
-// Register merge of row b by wave 0.  `st` holds slots t < G (the first 64
-// candidates of slice t, loaded with the summaries); slots G..G*TS-1 are
-// loaded here.  Returns the path code (0 done, 3 exact engine).
-template <int G>
+// Register merge of row b by wave 0.  The row's N filterable candidates sit
+// densely in LDS (`cc`); slot t of lane l holds candidate 64 t + l, so NS is
+// ceil(N / 64) rounded up to a compiled slot count.  `zc` is this lane's
+// share of the exact mass of the candidates left out of the store (those
+// below the min-p threshold, which no chain can keep); it counts towards the
+// normaliser only.  Returns the path code (0 done, 3 exact engine).
+template <int G, int NS>
 __device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& P, int b, const RowParams& rp,
-                                          const SliceHdr& hd, float m, float tcov, float ub, RegStore& st, int TS,
-                                          MergeSmem& sm) {
+                                          const SliceHdr& hd, float m, float tcov, float ub, const int2* cc, int N,
+                                          uint64_t zc, MergeSmem& sm) {
   const int lane = threadIdx.x & 63;
-  const int hn = lane < G ? hd.n : 0;
-  if (TS > 1) {
-    // second round trip: chunks 1.. of every slice (offsets < 8 * 64 <= cap)
-#pragma unroll
-    for (int t = 0; t < QM; ++t) {
-      if (t >= G) {
-        const int2 c = P.cand[((long long)b * G + t % G) * P.cap + (t / G) * 64 + lane];
-        st.cl[t] = __int_as_float(c.x);
-        st.ci[t] = c.y;
-      }
-    }
-  }
+  RegStore<NS> st;
   st.al = 0;
 #pragma unroll
-  for (int t = 0; t < QM; ++t) {
-    bool valid = false;
-    if (t < G * TS) {
-      const int ns = (int)lane_u32((uint32_t)hn, t % G);
-      valid = (t / G) * 64 + lane < ns;
-    }
-    st.cl[t] = valid ? st.cl[t] : -INFINITY;
-    st.ci[t] = valid ? st.ci[t] : -1;
+  for (int t = 0; t < NS; ++t) {
+    const bool valid = t * 64 + lane < N;
+    const int2 c = cc[valid ? t * 64 + lane : 0];
+    st.cl[t] = valid ? __int_as_float(c.x) : -INFINITY;
+    st.ci[t] = valid ? c.y : -1;
     st.al |= valid ? (1u << t) : 0u;
   }
+  // invalid slots hold -inf: exp_fix44 gives 0
 #pragma unroll
-  for (int t = 0; t < QM; ++t) st.w[t] = (t < G * TS && st.on(t)) ? exp_fix44(st.cl[t] - m) : 0ull;
+  for (int t = 0; t < NS; ++t) st.w[t] = exp_fix44(st.cl[t] - m);
+  uint64_t Scand;
   {
-    uint64_t mv[2] = {0ull, 0ull};
+    uint64_t mv[3] = {0ull, 0ull, zc};
 #pragma unroll
-    for (int t = 0; t < QM; ++t) {
+    for (int t = 0; t < NS; ++t) {
       mv[0] += st.w[t];
       mv[1] += st.cl[t] >= tcov ? st.w[t] : 0ull;
     }
-    wsum_u64_k<2>(mv);
+    wsum_u64_k<3>(mv);
     st.m_all = mv[0];
     st.m_cov = mv[1];
     st.cached = true;
+    Scand = mv[0] + mv[2];
   }
-  const uint64_t Scand = st.m_all;
   const ZBounds zb = z_bounds<G>(hd, lane < G, m, Scand);
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
 
@@ -1128,107 +1154,53 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& 
   const float Tc = (float)fmax((double)rp.T, 1e-5);
   if (rp.T != 1.0f) {
 #pragma unroll
-    for (int t = 0; t < QM; ++t)
-      st.w[t] = (t < G * TS && st.on(t)) ? exp_fix44(chain_scale(a.chain, st.cl[t] - m, invT, Tc)) : 0ull;
+    for (int t = 0; t < NS; ++t)
+      st.w[t] = st.on(t) ? exp_fix44(chain_scale(a.chain, st.cl[t] - m, invT, Tc)) : 0ull;
   }
-  // Slot t holds chunk t / G of slice t % G and slices are vocabulary
-  // ranges in order, so the per-slice kept masses locate the slice holding
-  // the target.  Inside that slice the candidates are in no order: each kept
-  // one is broadcast in turn (an s_ff1 walk over the kept lanes of each of
-  // the slice's slots) and every lane adds its weight to its own elements'
-  // inclusive sums when its id is not larger.  The draw is the smallest id
-  // whose inclusive sum exceeds the target.
-  uint64_t st_tot[G];
-#pragma unroll
-  for (int sl = 0; sl < G; ++sl) {
-    uint64_t v = 0;
-#pragma unroll
-    for (int t = sl; t < QM; t += G) v += (t < G * TS && st.on(t)) ? st.w[t] : 0ull;
-    st_tot[sl] = v;
-  }
-  wsum_u64_k<G>(st_tot);
+  // The draw is the smallest id whose inclusive kept weight, in vocabulary
+  // order, exceeds the target.  The candidates are in no order, so it is a
+  // radix descent over the 18-bit id, 6 bits per level: each level adds the
+  // kept weights of the ids under the current prefix into 64 LDS buckets,
+  // scans the buckets across the lanes, and takes the first bucket whose
+  // inclusive sum exceeds the remaining target.  Level 0 covers every kept
+  // candidate, so its scan total is the normaliser ZV.
   uint64_t ZV = 0;
+  uint32_t prefix = 0;
+  uint64_t rem = 0;
+  const int levels = a.tokens ? 3 : 1;
 #pragma unroll
-  for (int sl = 0; sl < G; ++sl) ZV += st_tot[sl];
-  const int nkept = st.count();
-  if (a.tokens) {
-    int tok = 0;
-    if (ZV) {
-      const uint64_t tgt = draw_target(ub, ZV);
-      uint64_t before = 0, rem = 0;
-      int ss = -1;
+  for (int lev = 0; lev < 3; ++lev) sm.bucket[lev][lane] = 0;
+  wave_sync();
+  for (int lev = 0; lev < levels; ++lev) {
+    const int s = 12 - 6 * lev;
 #pragma unroll
-      for (int sl = 0; sl < G; ++sl) {
-        if (ss < 0 && before + st_tot[sl] > tgt) {
-          ss = sl;
-          rem = tgt - before;
-        }
-        before += st_tot[sl];
-      }
-      // bucket the slice's kept weights by id (64 buckets of 2^sh ids), find
-      // the bucket holding the target with one prefix scan, then walk only
-      // that bucket's kept candidates
-      int sh = 0;
-      while (((P.SL - 1) >> sh) >= 64) ++sh;
-      const int v0s = ss * P.SL;
-      sm.bucket[lane] = 0;
-      wave_sync();
-#pragma unroll
-      for (int sl = 0; sl < G; ++sl) {
-        if (sl != ss) continue;
-#pragma unroll
-        for (int c = 0; c < QM / G; ++c) {
-          const int t = c * G + sl;
-          if (c < TS && st.on(t)) atomicAdd((unsigned long long*)&sm.bucket[(st.ci[t] - v0s) >> sh], (unsigned long long)st.w[t]);
-        }
-      }
-      wave_sync();
-      const uint64_t bv = sm.bucket[lane];
-      const uint64_t incl = wscan_u64(bv);
-      const uint64_t hitb = __ballot(incl > rem);
-      const int bsel = (int)__ffsll((long long)hitb) - 1;
-      const uint64_t rem2 = rem - (lane_u64(incl, bsel) - lane_u64(bv, bsel));
-      uint64_t cum[QM / G];
-#pragma unroll
-      for (int c = 0; c < QM / G; ++c) cum[c] = 0;
-#pragma unroll
-      for (int sl = 0; sl < G; ++sl) {
-        if (sl != ss) continue;
-        auto inb = [&](int t) { return st.on(t) && ((st.ci[t] - v0s) >> sh) == bsel; };
-#pragma unroll
-        for (int c = 0; c < QM / G; ++c) {
-          const int t = c * G + sl;
-          if (c >= TS) break;
-          uint64_t kept = __ballot(inb(t));
-          while (kept) {
-            const int j = (int)__ffsll((long long)kept) - 1;
-            kept &= kept - 1;
-            const uint32_t idj = lane_u32((uint32_t)st.ci[t], j);
-            const uint64_t wj = lane_u64(st.w[t], j);
-#pragma unroll
-            for (int c2 = 0; c2 < QM / G; ++c2) {
-              const int t2 = c2 * G + sl;
-              cum[c2] += (c2 < TS && (uint32_t)st.ci[t2] >= idj) ? wj : 0ull;
-            }
-          }
-        }
-        int best = 0x7FFFFFFF;
-#pragma unroll
-        for (int c = 0; c < QM / G; ++c) {
-          const int t = c * G + sl;
-          if (c < TS && inb(t) && cum[c] > rem2) best = min(best, st.ci[t]);
-        }
-        tok = wmin_i(best);
-      }
+    for (int t = 0; t < NS; ++t) {
+      if (st.on(t) && ((uint32_t)st.ci[t] >> (s + 6)) == prefix)
+        atomicAdd((unsigned long long*)&sm.bucket[lev][((uint32_t)st.ci[t] >> s) & 63u], (unsigned long long)st.w[t]);
     }
-    if (lane == 0) a.tokens[b] = tok;
+    wave_sync();
+    const uint64_t bv = sm.bucket[lev][lane];
+    const uint64_t incl = wscan_incl_u64(bv);
+    if (lev == 0) {
+      ZV = lane_u64(incl, 63);
+      if (!ZV) break;
+      rem = draw_target(ub, ZV);
+    }
+    // a bucket exists: rem is below the prefix's total
+    const int bsel = (int)__ffsll((long long)__ballot(incl > rem)) - 1;
+    rem -= lane_u64(incl, bsel) - lane_u64(bv, bsel);
+    prefix = (prefix << 6) | (uint32_t)bsel;
   }
-  if (lane == 0 && a.kept) a.kept[b] = nkept;
+  if (a.tokens && lane == 0) a.tokens[b] = ZV ? (int)prefix : 0;
+  if (a.kept) {
+    const int nkept = st.count();
+    if (lane == 0) a.kept[b] = nkept;
+  }
   float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
   if (out) {
     const double lz = log(ldexp((double)ZV, -44));
 #pragma unroll
-    for (int t = 0; t < QM; ++t)
+    for (int t = 0; t < NS; ++t)
       if (st.on(t))
         out[st.ci[t]] = a.out_mode == WH_OUT_MASKED ? st.cl[t]
                                                     : (float)((double)chain_scale(a.chain, st.cl[t] - m, invT, Tc) - lz);
@@ -1334,20 +1306,15 @@ __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
   if (tid < 64) {
     const int lane = tid;
     // one round trip: the summaries (lane s < G), the row's uniform and the
-    // first 64 candidates of every slice.  Every load is unconditional from a
-    // clamped, in-bounds address (lanes >= G and slots >= G read a duplicate
-    // that is ignored), so no branch join waits for a load to land.
+    // first QSPEC candidate chunks (slot t: chunk t / G of slice t % G).
+    // Every load is unconditional from an in-bounds address (lanes >= G read
+    // a duplicate summary, chunks past a slice's count stale entries, both
+    // ignored), so no branch join waits for a load to land.
     const SliceHdr hd = P.hdr[(long long)b * G + min(lane, G - 1)];
     const float ub = (a.tokens && !rp.greedy) ? a.u[b] : 0.0f;
-    RegStore st;
-    st.cached = false;
+    int2 spec[QSPEC];
 #pragma unroll
-    for (int t = 0; t < QM; ++t) {
-      int2 c = make_int2(0, -1);
-      if (t < QSPEC) c = P.cand[((long long)b * G + min(t, G - 1)) * P.cap + lane];
-      st.cl[t] = __int_as_float(c.x);
-      st.ci[t] = c.y;
-    }
+    for (int t = 0; t < QSPEC; ++t) spec[t] = P.cand[((long long)b * G + t % G) * P.cap + (t / G) * 64 + lane];
     // compiler barrier: keep every load above issued here, before anything
     // waits on the summaries (no hardware wait is implied)
     asm volatile("" ::: "memory");
@@ -1378,8 +1345,46 @@ __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
       path = 1;
     } else {
       const int TS = (nmax + 63) / 64;
-      if (G * TS <= QM && G <= QSPEC) path = merge_regs<G>(a, P, b, rp, hd, m, tcov, ub, st, TS, sm);
-      else path = merge_lds(&kernargs()->a, &kernargs()->p, b, rp, G, m, tcov, ub, dyn, &sm);
+      if (G * TS <= QSPEC) {
+        // Compact the loaded chunks into LDS.  Chunk t holds lanes
+        // [0, cnt_t) (a slice's candidates are a prefix of its list).  When
+        // min-p is the chain's last filter on the candidates (every chain but
+        // mlx_lm's top-k + top-p), a candidate below thr = m + ln min_p can
+        // never be kept: only its exact mass matters (to the normaliser), so
+        // it is summed here and left out.  Elsewhere thr is -inf and every
+        // candidate is filtered.
+        int2* cc = (int2*)dyn;
+        const bool split = rp.use_m && !(a.chain == WH_CHAIN_MLX && rp.use_k && rp.use_p);
+        const float thr = split ? m + min_p_log(a, rp.min_p) : -INFINITY;
+        const int hn = lane < G ? hd.n : 0;
+        int nsl[G];
+#pragma unroll
+        for (int l = 0; l < G; ++l) nsl[l] = (int)lane_u32((uint32_t)hn, l);
+        int N = 0;
+        uint64_t zc = 0;
+#pragma unroll
+        for (int t = 0; t < QSPEC; ++t) {
+          // cnt is wave uniform: empty chunks are skipped by a scalar branch
+          const int cnt = min(max(nsl[t % G] - (t / G) * 64, 0), 64);
+          if (cnt > 0) {
+            const float l = __int_as_float(spec[t].x);
+            const bool v = lane < cnt;
+            const bool hot = v && l >= thr;
+            if (split) zc += (v && !hot) ? exp_fix44(l - m) : 0ull;
+            const uint64_t bh = __ballot(hot);
+            if (hot) cc[N + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bh >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bh, 0u))] = spec[t];
+            N += (int)__popcll(bh);
+          }
+        }
+        wave_sync();
+        if (N <= 64) path = merge_regs<G, 1>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
+        else if (N <= 128) path = merge_regs<G, 2>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
+        else if (N <= 256) path = merge_regs<G, 4>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
+        else if (N <= 512) path = merge_regs<G, 8>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
+        else path = merge_regs<G, QM>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
+      } else {
+        path = merge_lds(&kernargs()->a, &kernargs()->p, b, rp, G, m, tcov, ub, dyn, &sm);
+      }
     }
     if (lane == 0) {
       s_path = path;
@@ -1395,27 +1400,36 @@ __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
 // Host side: plan, workspace layout, dispatch.
 // ---------------------------------------------------------------------------
 struct HostPlan {
-  int G, SL, R, cap, rule_cap, ept, pcap, codes_bytes, cand_off;
+  int G, SL, R, cap, rule_cap, ept, pcap, codes_bytes;
   size_t lds;
 };
+
+// Dynamic LDS of the slice kernel at most (its static LDS is under 1 KB).
+constexpr size_t SLICE_LDS_MAX = 160 * 1024 - 1024;
 
 static HostPlan make_plan(int B, int V, int dtype, int hcap) {
   HostPlan p;
   p.ept = dtype == WH_DTYPE_BF16 ? 8 : 4;
+  const int esz = dtype == WH_DTYPE_BF16 ? 2 : 4;
   const int slmax = FT * FAST_NE;
   const int bb = std::max(B, 1);
   int g = std::max(std::min((256 + bb - 1) / bb, GPREF), (V + slmax - 1) / slmax);
-  p.G = std::max(g, 1);
-  int sl = (V + p.G - 1) / p.G;
-  sl = (sl + p.ept - 1) / p.ept * p.ept;
-  p.SL = sl;
-  p.R = (sl + FT * p.ept - 1) / (FT * p.ept);
+  g = std::max(g, 1);
+  // more slices until the penalty codes (one per element) and the listed
+  // penalised elements fit in LDS
+  for (;; ++g) {
+    int sl = (V + g - 1) / g;
+    sl = (sl + p.ept - 1) / p.ept * p.ept;
+    p.G = g;
+    p.SL = sl;
+    p.codes_bytes = hcap > 0 ? (sl * esz + 15) / 16 * 16 : 0;
+    p.pcap = hcap > 0 ? std::min(hcap / 2, sl) : 0;
+    p.lds = (size_t)p.codes_bytes + (size_t)p.pcap * 8;
+    if (p.lds <= SLICE_LDS_MAX) break;
+  }
+  p.R = (p.SL + FT * p.ept - 1) / (FT * p.ept);
   p.cap = FAST_CAP;
   p.rule_cap = FAST_CAP / 2;
-  p.codes_bytes = hcap > 0 ? (sl * 2 + 15) / 16 * 16 : 0;
-  p.pcap = hcap > 0 ? std::min(hcap / 2, sl) : 0;
-  p.cand_off = p.codes_bytes + p.pcap * 8;
-  p.lds = (size_t)p.cand_off + (size_t)p.cap * sizeof(int2);
   return p;
 }
 
@@ -1433,11 +1447,14 @@ static WsLayout ws_layout(int B, const HostPlan& p) {
   return w;
 }
 
+// The largest layout over both element types, with and without penalties
+// (penalties can take more slices for the codes to fit in LDS).
 size_t sample_workspace_bytes(int B, int V) {
   if (B <= 0 || V <= 0) return 256;
-  WsLayout a = ws_layout(B, make_plan(B, V, WH_DTYPE_F32, 0));
-  WsLayout b = ws_layout(B, make_plan(B, V, WH_DTYPE_BF16, 0));
-  return std::max(a.total, b.total);
+  size_t t = 0;
+  for (int dt : {WH_DTYPE_F32, WH_DTYPE_BF16})
+    for (int hc : {0, 2 * WH_MAX_WINDOW}) t = std::max(t, ws_layout(B, make_plan(B, V, dt, hc)).total);
+  return t;
 }
 
 static int set_lds(const void* fn, size_t lds) {
@@ -1506,7 +1523,7 @@ int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st
   HostPlan hp = make_plan(k0.B, k0.V, k0.dtype, k0.hcap);
   WsLayout wl = ws_layout(k0.B, hp);
   const bool aligned = ((uintptr_t)k0.logits % 16 == 0) && ((k0.row_stride * esz) % 16 == 0) && (k0.V % hp.ept == 0);
-  if (!aligned || !p->workspace || p->workspace_bytes < wl.total) return launch_sample_exact(k0, st);
+  if (!aligned || !p->workspace || p->workspace_bytes < wl.total || hp.G > GMAX) return launch_sample_exact(k0, st);
   SampleKArgs k = k0;
   FastPlan fp;
   fp.G = hp.G;
@@ -1515,7 +1532,6 @@ int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st
   fp.rule_cap = hp.rule_cap;
   fp.pcap = hp.pcap;
   fp.codes_bytes = hp.codes_bytes;
-  fp.cand_off = hp.cand_off;
   char* ws = (char*)p->workspace;
   fp.path = (int*)(ws + wl.path);
   fp.hdr = (SliceHdr*)(ws + wl.hdr);
