@@ -264,6 +264,8 @@ struct OpSumI { __device__ int operator()(int a, int b) const { return a + b; } 
 struct OpSumU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a + b; } };
 struct OpSumF64 { __device__ double operator()(double a, double b) const { return a + b; } };
 struct OpMaxU32 { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
+struct OpMinU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a < b ? a : b; } };
+struct OpMaxU64 { __device__ uint64_t operator()(uint64_t a, uint64_t b) const { return a > b ? a : b; } };
 
 // Exclusive prefix sum of u64 across the block (thread order); returns the
 // exclusive prefix and writes the block total.

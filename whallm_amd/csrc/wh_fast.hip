@@ -58,7 +58,7 @@ constexpr int GPREF = 4;          // slices per row preferred for small batches
 constexpr int GMAX = 6;           // slices per row the merge is compiled for
 constexpr int FAST_CAP = 2048;    // candidate capacity per slice
 constexpr int RUNGS = 8;          // thresholds per ladder round
-constexpr int LADDER_ROUNDS = 4;  // ladder rounds at most (the first plus refinements)
+constexpr int LADDER_ROUNDS = 5;  // ladder rounds at most (the first, a far one, refinements)
 constexpr int QM = 16;            // merge: candidate slots per lane, at most
 constexpr int QSPEC = 16;         // merge: slots loaded speculatively with the summaries (slices <= 16)
 constexpr int HDR_OVERFLOW = 1;   // SliceHdr.flags: the row needs the exact engine
@@ -240,10 +240,14 @@ __device__ __forceinline__ void ladder_count(const float (&gm)[R], const int2* p
 #pragma unroll
     for (int j = 0; j < RUNGS; ++j) c[j] += v >= x[j] ? 1 : 0;
   }
+  // two rungs per reduction: a wave counts at most 64 * (R + 4) < 2^16
 #pragma unroll
-  for (int j = 0; j < RUNGS; ++j) {
-    const int w = wsum_i(c[j]);
-    if (lane == 0 && w) atomicAdd(&sm.lad[buf][j], w);
+  for (int j = 0; j < RUNGS; j += 2) {
+    const int w = wsum_i(c[j] | (c[j + 1] << 16));
+    if (lane == 0 && w) {
+      atomicAdd(&sm.lad[buf][j], w & 0xFFFF);
+      atomicAdd(&sm.lad[buf][j + 1], w >> 16);
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -255,7 +259,9 @@ __device__ __forceinline__ void ladder_count(const float (&gm)[R], const int2* p
 //   k > 0 (top-k bound): a threshold with at least k slice elements at or
 //     above it -- the highest rung whose group count reaches k (each counted
 //     group holds at least one such element), refined while the count
-//     exceeds max(2k, 64); -inf when no rung reaches k.
+//     exceeds max(2k, 64).  When no rung reaches k (an outlier far above the
+//     rest of the slice), a second round tries 2^11 .. 2^18 below the max;
+//     -inf when that fails too.
 //   k <= 0 (top-p alone): the lowest rung whose group count is at most half
 //     the buffer, refined once towards the next rung.
 template <int R>
@@ -285,8 +291,25 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
       }
       if (!found) hi = x[j];
     }
-    if (!found) return -INFINITY;
-    for (int round = 1; round < LADDER_ROUNDS && clo > target && hi != INFINITY; ++round) {
+    int round = 1;
+    if (!found) {
+      // fewer than k groups within 1024 of the max (an outlier far above the
+      // rest): rungs 2^11 .. 2^18 below it
+#pragma unroll
+      for (int j = 0; j < RUNGS; ++j) x[j] = ms - (float)(2048 << j);
+      ladder_count<R>(gm, patch, npatch, x, c, round++, sm);
+#pragma unroll
+      for (int j = 0; j < RUNGS; ++j) {
+        if (!found && c[j] >= k) {
+          found = true;
+          lo = x[j];
+          clo = c[j];
+        }
+        if (!found) hi = x[j];
+      }
+      if (!found) return -INFINITY;
+    }
+    for (; round < LADDER_ROUNDS && clo > target && hi != INFINITY; ++round) {
       const float span = hi - lo;
 #pragma unroll
       for (int q = 0; q < RUNGS; ++q) x[q] = hi - span * (float)(q + 1) / (float)(RUNGS + 1);
@@ -758,31 +781,6 @@ __device__ __forceinline__ ZBounds z_bounds(const SliceHdr& hd, bool own, float 
   return z;
 }
 
-// Bits common to lo and hi above their highest differing bit (lower bits
-// cleared), and the number of bits below that point.  Written with shifts by
-// constants only.
-__device__ __forceinline__ uint32_t common_prefix(uint32_t lo, uint32_t hi, int& nbits) {
-  uint32_t d = lo ^ hi;
-  d |= d >> 1;
-  d |= d >> 2;
-  d |= d >> 4;
-  d |= d >> 8;
-  d |= d >> 16;
-  nbits = __popc(d);
-  return lo & ~d;
-}
-
-// Inclusive prefix sum over the wave's lanes (lane order).
-__device__ __forceinline__ uint64_t wscan_u64(uint64_t x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint64_t y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
-
 // Candidates in registers: NS slots per lane (a compile-time count, so every
 // loop over the slots is straight-line code), alive bits in `al`.
 template <int NS>
@@ -791,6 +789,7 @@ struct RegStore {
   int ci[NS];
   uint64_t w[NS];  // exp_fix44(l - m) (replaced by the draw weights at the end)
   uint32_t al;
+  uint64_t* bkt;  // 64 LDS buckets for the radix descents
   // masses of the alive set (all / covered) while no filter has changed it
   bool cached;
   uint64_t m_all, m_cov;
@@ -818,36 +817,6 @@ struct RegStore {
     al = m;
     cached = false;
   }
-  // Smallest / largest key and id over alive slots where f holds (wave).
-  template <typename F>
-  __device__ __forceinline__ void key_range(F f, uint32_t& kmn, uint32_t& kmx) const {
-    kmn = 0xFFFFFFFFu;
-    kmx = 0u;
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-      const uint32_t k = fkey(cl[t]);
-      const bool p = on(t) && f(t);
-      kmn = p && k < kmn ? k : kmn;
-      kmx = p && k > kmx ? k : kmx;
-    }
-    kmn = wmin_u32(kmn);
-    kmx = wmax_u32(kmx);
-  }
-  template <typename F>
-  __device__ __forceinline__ void id_range(F f, uint32_t& imn, uint32_t& imx) const {
-    imn = 0xFFFFFFFFu;
-    imx = 0u;
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-      const uint32_t i = (uint32_t)ci[t];
-      const bool p = on(t) && f(t);
-      imn = p && i < imn ? i : imn;
-      imx = p && i > imx ? i : imx;
-    }
-    imn = wmin_u32(imn);
-    imx = wmax_u32(imx);
-  }
-
   __device__ __forceinline__ int count() const { return count_if([](int) { return true; }); }
   __device__ __forceinline__ uint64_t mass(bool cov_only, float tcov) const {
     if (cached) return cov_only ? m_cov : m_all;
@@ -860,167 +829,132 @@ struct RegStore {
   __device__ __forceinline__ void keep_min(float thr) {
     keep_if([&](int t) { return cl[t] >= thr; });
   }
+  // The composite (order ORD) of the element at which the cumulative measure
+  // (count, or mass when MASS) over the alive slots where f holds first
+  // reaches target (0 < target <= total), in descending composite order.  A
+  // radix descent, 6 bits per level below the bits every such composite
+  // shares: each level adds the measures of the slots under the current
+  // prefix into 64 LDS buckets (bucket d at lane 63 - d, so lane order is
+  // descending), scans the lanes and takes the first bucket whose inclusive
+  // sum reaches the remaining target.
+  template <int ORD, bool MASS, typename F>
+  __device__ __forceinline__ uint64_t select_desc(F f, uint64_t target, uint64_t* bucket) const {
+    const int lane = threadIdx.x & 63;
+    uint64_t c[NS];
+    uint64_t cmin = ~0ull, cmax = 0ull;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      const uint32_t k = fkey(cl[t]);
+      c[t] = ORD == ORD_P ? comp_p(k, ci[t]) : comp_a(k, ci[t]);
+      const bool p = on(t) && f(t);
+      cmin = p && c[t] < cmin ? c[t] : cmin;
+      cmax = p && c[t] > cmax ? c[t] : cmax;
+    }
+    cmin = dpp_reduce_u64(cmin, [](uint64_t x, uint64_t y) { return x < y ? x : y; });
+    cmax = dpp_reduce_u64(cmax, [](uint64_t x, uint64_t y) { return x > y ? x : y; });
+    const uint64_t diff = cmin ^ cmax;
+    const int top = diff ? 64 - __clzll((long long)diff) : 1;
+    const int L = (top + 5) / 6;
+    uint64_t prefix = cmax >> (6 * L);
+    for (int lev = 0; lev < L; ++lev) {
+      const int sh = 6 * (L - 1 - lev);
+      bucket[lane] = 0;
+      wave_sync();
+#pragma unroll
+      for (int t = 0; t < NS; ++t) {
+        if (on(t) && f(t) && (c[t] >> (sh + 6)) == prefix)
+          atomicAdd((unsigned long long*)&bucket[63 - (int)((c[t] >> sh) & 63)], (unsigned long long)(MASS ? w[t] : 1ull));
+      }
+      wave_sync();
+      const uint64_t bv = bucket[lane];
+      const uint64_t incl = wscan_incl_u64(bv);
+      const int sel = (int)__ffsll((long long)__ballot(incl >= target)) - 1;
+      target -= lane_u64(incl, sel) - lane_u64(bv, sel);
+      prefix = (prefix << 6) | (uint64_t)(63 - sel);
+      wave_sync();
+    }
+    return prefix;
+  }
   // Top-k in order A (value desc, id asc) over the alive slots.
   __device__ __forceinline__ void keep_topk(int k) {
     if (count() <= k) return;
-    uint32_t kmn, kmx;
-    key_range([](int) { return true; }, kmn, kmx);
-    int nb;
-    uint32_t x = common_prefix(kmn, kmx, nb);
-    // largest x with #(key >= x) >= k: the k-th largest key
-    for (int bit = nb - 1; bit >= 0; --bit) {
-      const uint32_t tr = x | (1u << bit);
-      if (count_if([&](int t) { return fkey(cl[t]) >= tr; }) >= k) x = tr;
-    }
-    const uint32_t v = x;
-    const int need = k - count_if([&](int t) { return fkey(cl[t]) > v; });
-    const int ce = count_if([&](int t) { return fkey(cl[t]) == v; });
-    if (ce <= need) {
-      keep_if([&](int t) { return fkey(cl[t]) >= v; });
-      return;
-    }
-    // ties at v: keep the `need` lowest ids
-    uint32_t imn, imx;
-    id_range([&](int t) { return fkey(cl[t]) == v; }, imn, imx);
-    int ni;
-    uint32_t z = common_prefix(imn, imx, ni);
-    for (int bit = ni - 1; bit >= 0; --bit) {
-      const uint32_t tr = z | (1u << bit);
-      if (count_if([&](int t) { return fkey(cl[t]) == v && (uint32_t)ci[t] < tr; }) < need) z = tr;
-    }
-    keep_if([&](int t) {
-      const uint32_t k2 = fkey(cl[t]);
-      return k2 > v || (k2 == v && (uint32_t)ci[t] <= z);
-    });
+    const uint64_t ck = select_desc<ORD_A, false>([](int) { return true; }, (uint64_t)k, bkt);
+    keep_if([&](int t) { return comp_a(fkey(cl[t]), ci[t]) >= ck; });
   }
-  // The element (order P: value desc, id desc) at which the cumulative mass
-  // over alive covered slots first reaches R (0 < R <= that mass).
-  __device__ __forceinline__ void p_cut(uint64_t R, float tcov, uint32_t& vk, uint32_t& vid) const {
-    auto cov = [&](int t) { return cl[t] >= tcov; };
-    uint32_t kmn, kmx;
-    key_range(cov, kmn, kmx);
-    int nb;
-    uint32_t x = common_prefix(kmn, kmx, nb);
-    for (int bit = nb - 1; bit >= 0; --bit) {
-      const uint32_t tr = x | (1u << bit);
-      if (mass_if([&](int t) { return cov(t) && fkey(cl[t]) >= tr; }) >= R) x = tr;
-    }
-    const uint32_t v = x;
-    const uint64_t need = R - mass_if([&](int t) { return cov(t) && fkey(cl[t]) > v; });
-    uint32_t imn, imx;
-    id_range([&](int t) { return cov(t) && fkey(cl[t]) == v; }, imn, imx);
-    int ni;
-    uint32_t y = common_prefix(imn, imx, ni);
-    // largest y with mass(ties with id >= y) >= need
-    for (int bit = ni - 1; bit >= 0; --bit) {
-      const uint32_t tr = y | (1u << bit);
-      if (mass_if([&](int t) { return cov(t) && fkey(cl[t]) == v && (uint32_t)ci[t] >= tr; }) >= need) y = tr;
-    }
-    vk = v;
-    vid = y;
-  }
+  // Top-p cut over the alive covered slots: both ends of [Rlo, Rhi] must
+  // select the same element (order P).
   __device__ __forceinline__ bool keep_pcut(uint64_t Rlo, uint64_t Rhi, float tcov) {
-    uint32_t k0, i0, k1, i1;
-    p_cut(Rlo, tcov, k0, i0);
-    p_cut(Rhi, tcov, k1, i1);
-    if (k0 != k1 || i0 != i1) return false;
-    keep_if([&](int t) {
-      const uint32_t k = fkey(cl[t]);
-      return k > k0 || (k == k0 && (uint32_t)ci[t] >= i0);
-    });
+    auto cov = [&](int t) { return cl[t] >= tcov; };
+    const uint64_t clo = select_desc<ORD_P, true>(cov, Rlo, bkt);
+    const uint64_t chi = select_desc<ORD_P, true>(cov, Rhi, bkt);
+    if (clo != chi) return false;
+    keep_if([&](int t) { return comp_p(fkey(cl[t]), ci[t]) >= clo; });
     return true;
   }
 };
 
-// Candidates in LDS (any number), walked by wave 0.
+// Register merge scratch.
 struct MergeSmem {
-  uint64_t hist[1024];
-  uint64_t bc64[2];
-  uint64_t bucket[3][64];  // register merge: draw buckets, one array per radix level
+  uint64_t bucket[3][64];  // draw buckets, one array per radix level
 };
 
-struct WaveCands {
-  const float* v;
-  const int* id;
-  int n;
-  template <typename F>
-  __device__ __forceinline__ void each(F f) const {
-    for (int j = (int)(threadIdx.x & 63); j < n; j += 64) f(id[j], v[j]);
-  }
-};
-
-// Wave-level radix select (same contract as radix_select): the composite of
-// the element at which the cumulative measure over kept candidates first
-// reaches target (0 < target <= total).  Digits start below the bits common
-// to every kept composite.
-template <int ORD, typename Meas>
-__device__ uint64_t wave_radix_select(const WaveCands& src, const Pred& pr, Meas meas, uint64_t target, MergeSmem& sm) {
-  const int lane = threadIdx.x & 63;
-  uint64_t cmin = ~0ull, cmax = 0;
-  src.each([&](int i, float l) {
-    if (!pr.keep(i, l)) return;
-    const uint64_t c = composite<ORD>(l, i);
-    cmin = c < cmin ? c : cmin;
-    cmax = c > cmax ? c : cmax;
-  });
-  cmin = dpp_reduce_u64(cmin, [](uint64_t a, uint64_t b) { return a < b ? a : b; });
-  cmax = dpp_reduce_u64(cmax, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
-  if (cmax < cmin) return 0;
-  const uint64_t diff = cmin ^ cmax;
-  const int top = diff ? 64 - __clzll((long long)diff) : 1;
-  const int PASSES = (top + 9) / 10;
-  uint64_t prefix = cmax >> (10 * PASSES);
-  for (int pass = 0; pass < PASSES; ++pass) {
-    const int shift = 10 * (PASSES - 1 - pass);
-    for (int i = lane; i < 1024; i += 64) sm.hist[i] = 0;
-    wave_sync();
-    src.each([&](int i, float l) {
-      if (!pr.keep(i, l)) return;
-      const uint64_t c = composite<ORD>(l, i);
-      if ((c >> (shift + 10)) != prefix) return;
-      const uint64_t w = meas(i, l);
-      if (w) atomicAdd((unsigned long long*)&sm.hist[(c >> shift) & 1023], (unsigned long long)w);
-    });
-    wave_sync();
-    // lane owns bins 1023-16*lane .. 1008-16*lane (descending)
-    uint64_t ls = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) ls += sm.hist[1023 - 16 * lane - q];
-    uint64_t incl = ls;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t y = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += y;
-    }
-    uint64_t c = incl - ls;
-    if (c < target && incl >= target) {
-      for (int q = 0; q < 16; ++q) {
-        const uint64_t hv = sm.hist[1023 - 16 * lane - q];
-        if (c < target && c + hv >= target) {
-          sm.bc64[0] = (uint64_t)(1023 - 16 * lane - q);
-          sm.bc64[1] = c;
-        }
-        c += hv;
+// Normaliser bounds for the block merge: the same computation as z_bounds,
+// every thread reading the G summaries itself.
+__device__ __forceinline__ ZBounds z_bounds_loop(const SliceHdr* hd, int G, float m, uint64_t Scand) {
+  const double SC = 17592186044416.0, EPS = 2e-4;
+  double slo = 0.0, shi = 0.0, szl = 0.0, szh = 0.0;
+  int nz = 0;
+  for (int l = 0; l < G; ++l) {
+    const SliceHdr& h = hd[l];
+    double lo = 0.0, hi = 0.0, zl = 0.0, zh = 0.0;
+    int no_zf = 0;
+    if (h.m != -INFINITY) {
+      auto wlo = [&](float t) {
+        return t == -INFINITY ? 0.0 : fmax(floor((double)expf(t - m) * SC * (1.0 - EPS)) - 1.0, 0.0);
+      };
+      lo = (double)h.g1 * wlo(h.t1) + (double)h.g2 * wlo(h.t2);
+      hi = (double)(h.nall - h.n) * ((double)expf(h.tau - m) * SC * (1.0 + EPS) + 1.0);
+      if (h.zf >= 0.0) {
+        const double sc = (double)expf(h.m - m) * SC;
+        zl = h.zf * sc * (1.0 - EPS) - (double)h.nall;
+        zh = h.zf * sc * (1.0 + EPS) + (double)h.nall;
+      } else {
+        no_zf = 1;
       }
     }
-    wave_sync();
-    prefix = (prefix << 10) | sm.bc64[0];
-    target -= sm.bc64[1];
-    wave_sync();
+    slo += lo;
+    shi += hi;
+    szl += zl;
+    szh += zh;
+    nz += no_zf;
   }
-  return prefix;
+  const double LIM = 4.0e18;
+  ZBounds z;
+  z.lo = Scand + (uint64_t)fmax(slo, 0.0);
+  z.hi = (shi >= LIM) ? (1ull << 62) : Scand + (uint64_t)ceil(shi);
+  if (nz == 0) {
+    const uint64_t a = szl <= 0.0 ? 0ull : (uint64_t)szl;
+    const uint64_t c = szh >= LIM ? (1ull << 62) : (uint64_t)ceil(szh);
+    z.lo = a > z.lo ? a : z.lo;
+    z.hi = c < z.hi ? c : z.hi;
+  }
+  if (z.hi > (1ull << 62)) z.hi = 1ull << 62;
+  return z;
 }
 
-struct LdsStore {
-  WaveCands src;
+// Candidates in LDS (any number), filtered by the whole workgroup: counts and
+// masses are block reductions, cut points block radix selects.  Every method
+// is called by every thread.
+struct BlockStore {
+  CandSource src;
   Pred pr;
   float m;
-  MergeSmem* sm;
+  ExactSmem* sm;
 
   __device__ __forceinline__ int count() const {
     int c = 0;
     src.each([&](int i, float l) { c += pr.keep(i, l) ? 1 : 0; });
-    return wsum_i(c);
+    return block_reduce(c, sm->scratchi, OpSumI(), 0);
   }
   __device__ __forceinline__ uint64_t mass(bool cov_only, float tcov) const {
     Pred p = pr;
@@ -1028,7 +962,7 @@ struct LdsStore {
     uint64_t z = 0;
     const float mm = m;
     src.each([&](int i, float l) { if (p.keep(i, l)) z += exp_fix44(l - mm); });
-    return wsum_u64(z);
+    return block_reduce(z, sm->scratch64, OpSumU64(), (uint64_t)0);
   }
   __device__ __forceinline__ void none() { pr.none = 1; }
   __device__ __forceinline__ void keep_min(float thr) {
@@ -1037,7 +971,7 @@ struct LdsStore {
   }
   __device__ __forceinline__ void keep_topk(int k) {
     if (count() <= k) return;
-    const uint64_t ck = wave_radix_select<ORD_A>(src, pr, [](int, float) { return (uint64_t)1; }, (uint64_t)k, *sm);
+    const uint64_t ck = radix_select<ORD_A, true>(src, pr, [](int, float) { return (uint64_t)1; }, (uint64_t)k, *sm);
     pr.use_k = 1;
     pr.ck = ck;
   }
@@ -1046,8 +980,8 @@ struct LdsStore {
     pc.cov = tcov;
     const float mm = m;
     auto mass_fn = [mm](int, float l) { return exp_fix44(l - mm); };
-    const uint64_t clo = wave_radix_select<ORD_P>(src, pc, mass_fn, Rlo, *sm);
-    const uint64_t chi = wave_radix_select<ORD_P>(src, pc, mass_fn, Rhi, *sm);
+    const uint64_t clo = radix_select<ORD_P, true>(src, pc, mass_fn, Rlo, *sm);
+    const uint64_t chi = radix_select<ORD_P, true>(src, pc, mass_fn, Rhi, *sm);
     if (clo != chi) return false;
     pr.use_p = 1;
     pr.cp = clo;
@@ -1121,6 +1055,7 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& 
   const int lane = threadIdx.x & 63;
   RegStore<NS> st;
   st.al = 0;
+  st.bkt = sm.bucket[0];
 #pragma unroll
   for (int t = 0; t < NS; ++t) {
     const bool valid = t * 64 + lane < N;
@@ -1208,79 +1143,64 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& 
   return 0;
 }
 
-// LDS merge of row b by wave 0 (any number of candidates).  Returns the path
-// code (4 done, 3 exact engine).
-// The arguments are read in place from the kernel-argument segment (a
-// pointer, not a copy), so calling this out-of-line path forces nothing of
-// the caller's into private memory.
-__device__ __noinline__ int merge_lds(const SampleKArgs* ap, const FastPlan* pp, int b, RowParams rp, int G, float m,
-                                      float tcov, float ub, char* dyn, MergeSmem* smp) {
+// Block merge of row b (any number of candidates), run by every thread of
+// the workgroup.  Returns the path code (4 done, 3 exact engine).  The
+// arguments are read in place from the kernel-argument segment (a pointer,
+// not a copy), so calling this out-of-line path forces nothing of the
+// caller's into private memory.
+__device__ __noinline__ int merge_block(const SampleKArgs* ap, const FastPlan* pp, int b, RowParams rp, int G, float m,
+                                       float tcov, float ub, char* dyn, ExactSmem* smp) {
   const SampleKArgs& a = *ap;
   const FastPlan& P = *pp;
-  MergeSmem& sm = *smp;
-  const int lane = threadIdx.x & 63;
-  SliceHdr hd;
-  if (lane < G) hd = P.hdr[(long long)b * G + lane];
-  const int hn = lane < G ? hd.n : 0;
+  ExactSmem& sm = *smp;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const SliceHdr* hd = P.hdr + (long long)b * G;
   float* cv = (float*)dyn;
   int* ci = (int*)(dyn + (size_t)G * P.cap * sizeof(float));
-  int off = hn;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(off, o, 64);
-    if (lane >= o) off += y;
-  }
-  const int N = __shfl(off, 63, 64);
-  off -= hn;
+  int N = 0;
   for (int s = 0; s < G; ++s) {
-    const int ns = __shfl(hn, s, 64), os = __shfl(off, s, 64);
+    const int ns = hd[s].n;
     const int2* src = P.cand + ((long long)b * G + s) * P.cap;
-    for (int j = lane; j < ns; j += 64) {
+    for (int j = tid; j < ns; j += nt) {
       const int2 c = src[j];
-      cv[os + j] = __int_as_float(c.x);
-      ci[os + j] = c.y;
+      cv[N + j] = __int_as_float(c.x);
+      ci[N + j] = c.y;
     }
+    N += ns;
   }
-  wave_sync();
-  LdsStore st;
-  st.src = WaveCands{cv, ci, N};
+  __syncthreads();
+  BlockStore st;
+  st.src = CandSource{cv, ci, N};
   st.pr = Pred{0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
   st.m = m;
   st.sm = &sm;
   const uint64_t Scand = st.mass(false, 0.0f);
-  ZBounds zb;
-  switch (G) {
-    case 1: zb = z_bounds<1>(hd, lane < G, m, Scand); break;
-    case 2: zb = z_bounds<2>(hd, lane < G, m, Scand); break;
-    case 3: zb = z_bounds<3>(hd, lane < G, m, Scand); break;
-    case 4: zb = z_bounds<4>(hd, lane < G, m, Scand); break;
-    case 5: zb = z_bounds<5>(hd, lane < G, m, Scand); break;
-    case 6: zb = z_bounds<6>(hd, lane < G, m, Scand); break;
-    case 7: zb = z_bounds<7>(hd, lane < G, m, Scand); break;
-    default: zb = z_bounds<8>(hd, lane < G, m, Scand); break;
-  }
+  const ZBounds zb = z_bounds_loop(hd, G, m, Scand);
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
   const float invT = (float)(1.0 / (double)rp.T);
   const float Tc = (float)fmax((double)rp.T, 1e-5);
   const Pred pr = st.pr;
-  const WaveCands src = st.src;
+  const CandSource src = st.src;
   auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, Tc)); };
   uint64_t zv = 0;
   int nk = 0;
   src.each([&](int i, float l) {
-    if (pr.keep(i, l)) { zv += vw(i, l); ++nk; }
+    if (pr.keep(i, l)) {
+      zv += vw(i, l);
+      ++nk;
+    }
   });
-  const uint64_t ZV = wsum_u64(zv);
-  const int nkept = wsum_i(nk);
+  const uint64_t ZV = block_reduce(zv, sm.scratch64, OpSumU64(), (uint64_t)0);
+  const int nkept = block_reduce(nk, sm.scratchi, OpSumI(), 0);
   if (a.tokens) {
     int tok = 0;
     if (ZV) {
       const uint64_t tgt = draw_target(ub, ZV);
-      tok = 0x3FFFF - (int)wave_radix_select<ORD_ID>(src, pr, vw, tgt + 1, sm);
+      tok = 0x3FFFF - (int)radix_select<ORD_ID, true>(src, pr, vw, tgt + 1, sm);
     }
-    if (lane == 0) a.tokens[b] = tok;
+    if (tid == 0) a.tokens[b] = tok;
   }
-  if (lane == 0 && a.kept) a.kept[b] = nkept;
+  if (tid == 0 && a.kept) a.kept[b] = nkept;
   float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
   if (out) {
     const double lz = log(ldexp((double)ZV, -44));
@@ -1292,13 +1212,13 @@ __device__ __noinline__ int merge_lds(const SampleKArgs* ap, const FastPlan* pp,
   return 4;
 }
 
-
 template <int G>
 __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ ExactSmem esm;
   __shared__ MergeSmem sm;
   __shared__ int s_path;
+  __shared__ float s_m, s_tcov, s_ub;
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const RowRaw raw = row_raw(a, b);
@@ -1383,16 +1303,26 @@ __global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
         else if (N <= 512) path = merge_regs<G, 8>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
         else path = merge_regs<G, QM>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
       } else {
-        path = merge_lds(&kernargs()->a, &kernargs()->p, b, rp, G, m, tcov, ub, dyn, &sm);
+        path = 5;  // too many for registers: the whole workgroup merges
+        if (lane == 0) {
+          s_m = m;
+          s_tcov = tcov;
+          s_ub = ub;
+        }
       }
     }
     if (lane == 0) {
       s_path = path;
-      P.path[b] = path;
+      if (path != 5) P.path[b] = path;
     }
   }
   __syncthreads();
-  const int path = s_path;
+  int path = s_path;
+  if (path == 5) {
+    path = merge_block(&kernargs()->a, &kernargs()->p, b, rp, G, s_m, s_tcov, s_ub, dyn, &esm);
+    if (tid == 0) P.path[b] = path;
+    __syncthreads();
+  }
   if (path == 1 || path == 3) exact_row(kernargs()->a, b, dyn, esm);
 }
 

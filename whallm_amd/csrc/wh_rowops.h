@@ -158,12 +158,31 @@ __device__ __forceinline__ uint64_t composite(float l, int i) {
 // ORD_P: value desc, id desc; ORD_ID: id asc).  Returns the composite of
 // the element at which the cumulative measure meas(i, l) over elements kept
 // by `pr` first reaches `target` (0 < target <= total).  10-bit digits: five
-// passes for the 50-bit value/id composites, two for ORD_ID.
-template <int ORD, typename Src, typename Meas>
+// passes for the 50-bit value/id composites, two for ORD_ID.  With SKIP (for
+// short candidate lists, whose composites often share their top bits), one
+// min/max pass first drops the digits every kept composite shares, which
+// would otherwise send every atomic of a pass to one bin.
+template <int ORD, bool SKIP = false, typename Src, typename Meas>
 __device__ uint64_t radix_select(const Src& src, const Pred& pr, Meas meas, uint64_t target, ExactSmem& sm) {
   const int tid = threadIdx.x;
-  constexpr int PASSES = ORD == ORD_ID ? 2 : 5;
+  int PASSES = ORD == ORD_ID ? 2 : 5;
   uint64_t prefix = 0;
+  if (SKIP) {
+    uint64_t cmin = ~0ull, cmax = 0;
+    src.each([&](int i, float l) {
+      if (!pr.keep(i, l)) return;
+      const uint64_t c = composite<ORD>(l, i);
+      cmin = c < cmin ? c : cmin;
+      cmax = c > cmax ? c : cmax;
+    });
+    cmin = block_reduce(cmin, sm.scratch64, OpMinU64(), (uint64_t)~0ull);
+    cmax = block_reduce(cmax, sm.scratch64, OpMaxU64(), (uint64_t)0);
+    if (cmax < cmin) return 0;
+    const uint64_t diff = cmin ^ cmax;
+    const int top = diff ? 64 - __clzll((long long)diff) : 1;
+    PASSES = (top + 9) / 10;
+    prefix = cmax >> (10 * PASSES);
+  }
   for (int pass = 0; pass < PASSES; ++pass) {
     const int shift = 10 * (PASSES - 1 - pass);
     for (int i = tid; i < 1024; i += blockDim.x) sm.hist[i] = 0;
