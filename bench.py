@@ -13,6 +13,7 @@ with HIP events on the launch stream), and the CPU baseline (the oracle's
 float32 replay of the reference op order, timed on this host's cores).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 2]
+    python bench.py --workload 3         # the fused speculative verifier
     python bench.py --copy-calibration   # plain 256 MiB copies, for PMC scaling
 """
 from __future__ import annotations
@@ -37,7 +38,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 4, 5])
+    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--sets", type=int, default=16)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -94,6 +95,106 @@ def make_sets(w, nsets, dev):
     return sets
 
 
+def make_verify_sets(w, nsets, dev):
+    """Verify input sets: set 0 is the seeded workload; sets 1.. are fresh
+    draws on the device (target ~N(0, 2.5^2), draft = target + N(0, 0.5^2)
+    tempered and softmaxed, draft ids drawn from the draft)."""
+    import torch
+
+    sets = []
+    for s in range(nsets):
+        if s == 0:
+            tgt = torch.from_numpy(w.target_logits).to(dev)
+            q = torch.from_numpy(w.draft_q).to(dev)
+            toks = torch.from_numpy(w.draft_tokens).to(dev)
+        else:
+            g = torch.Generator(device=dev)
+            g.manual_seed(2000 + s)
+            tgt = torch.randn(w.B, w.n + 1, w.V, device=dev, generator=g) * 2.5
+            dl = tgt[:, :w.n] + torch.randn(w.B, w.n, w.V, device=dev, generator=g) * 0.5
+            q = torch.softmax(dl / w.temperature, dim=-1)
+            toks = torch.multinomial(q.reshape(-1, w.V), 1, generator=g).reshape(w.B, w.n).to(torch.int32)
+        sets.append((tgt.contiguous(), q.contiguous(), toks.contiguous()))
+    return sets
+
+
+def bench_verify(args):
+    """Workload 3: the fused speculative verifier (wh_verify_fused)."""
+    import torch
+
+    from oracle import oracle as o
+    from whallm_amd import sampling, synth
+
+    dev = torch.device("cuda:0")
+    w = synth.workload3()
+    sets = make_verify_sets(w, args.sets, dev)
+    u = torch.from_numpy(w.uniforms).to(dev)
+    want_a, want_t = o.verify_fused(w.target_logits, w.draft_q, w.draft_tokens, w.uniforms, w.temperature)
+    calls = [sampling.VerifyCall(t, q, k, w.temperature, u) for t, q, k in sets]
+    a0, t0 = calls[0]()
+    parity = {"rows": int(w.B), "contract_bit_exact": bool(np.array_equal(a0.cpu().numpy(), want_a)
+                                                          and np.array_equal(t0.cpu().numpy(), want_t)),
+              "accepted_mean": float(np.mean(want_a))}
+    for i in range(args.warmup):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0w = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.steps):
+        calls[i % len(calls)]()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0w
+    avg_s = e0.elapsed_time(e1) / 1e3 / args.steps
+    a1, t1 = calls[0]()
+    parity["timed_set0_bit_exact"] = bool(np.array_equal(a1.cpu().numpy(), want_a) and np.array_equal(t1.cpu().numpy(), want_t))
+    nbytes = w.bytes_per_call()
+    achieved = nbytes / avg_s / 1e9
+    traffic, traffic_src = measured_traffic(3, w.name)
+    res = {
+        "metric": "verified rows/sec + % of HBM peak, speculative verify at B=16, n=8, V=129,280",
+        "value": w.B * args.steps / wall,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": w.name, "B": w.B, "n": w.n, "V": w.V, "input_sets": len(sets),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                     "kernel": "wh_verify_fused", "kernel_avg_us": avg_s * 1e6, "algorithmic_bytes": nbytes,
+                     "traffic_source": traffic_src},
+        "parity": parity,
+    }
+    if not args.no_cpu_baseline:
+        try:
+            cores = len(os.sched_getaffinity(0))
+        except AttributeError:
+            cores = os.cpu_count() or 1
+        threads = max(1, min(cores, 16))
+        rows = 0
+        t0c = time.perf_counter()
+        while True:
+            o.verify_fused(w.target_logits, w.draft_q, w.draft_tokens, w.uniforms, w.temperature, threads=threads)
+            rows += w.B
+            el = time.perf_counter() - t0c
+            if el >= args.cpu_seconds:
+                break
+        res["cpu_baseline"] = {"value": rows / el, "unit": "rows/s", "cores": threads, "kind": "port",
+                               "sample": f"{rows} rows ({rows // w.B} passes over the seeded batch), the oracle's "
+                                         f"verify contract, OpenMP over rows, {el:.1f} s; host reports {cores} usable cores"}
+    print(json.dumps(res))
+
+
 def measured_traffic(workload: int, name: str):
     """HBM bytes per call from the committed rocprofv3 --pmc summary of this
     workload (FETCH_SIZE and WRITE_SIZE runs, each scaled by what the counter
@@ -142,6 +243,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+    if args.workload == 3:
+        bench_verify(args)
         return
     import torch
 

@@ -335,6 +335,46 @@ def verify_fused(target_logits: torch.Tensor, draft_probs: torch.Tensor, draft_t
     return acc, tok
 
 
+class VerifyCall:
+    """A wh_verify_fused launch bound to fixed device buffers (target logits
+    [B, n+1, V], draft probabilities [B, n, V], draft tokens [B, n],
+    uniforms [B, n+1]); each call is one ctypes call on the stream current at
+    construction.  Outputs are the attributes `accepted` and `token`."""
+
+    def __init__(self, target_logits: torch.Tensor, draft_probs: torch.Tensor, draft_tokens: torch.Tensor,
+                 temperature: float, uniforms: torch.Tensor):
+        target = target_logits
+        if target.dtype != torch.float32 or not target.is_contiguous():
+            raise ValueError("target logits must be a contiguous float32 [B, n+1, V] buffer")
+        B, n1, V = target.shape
+        n = n1 - 1
+        dev = target.device
+        q = draft_probs if n > 0 else None
+        if q is not None and (q.dtype != torch.float32 or not q.is_contiguous() or tuple(q.shape) != (B, n, V)):
+            raise ValueError("draft probabilities must be a contiguous float32 [B, n, V] buffer")
+        toks = torch.as_tensor(draft_tokens, dtype=torch.int32, device=dev).reshape(B, n)
+        u = torch.as_tensor(uniforms, dtype=torch.float32, device=dev).reshape(B, n1)
+        if not toks.is_contiguous() or not u.is_contiguous():
+            raise ValueError("draft tokens and uniforms must be contiguous buffers")
+        L.require_device(target, q, toks, u)
+        self.accepted = torch.empty(B, dtype=torch.int32, device=dev)
+        self.token = torch.empty(B, dtype=torch.int32, device=dev)
+        self.args = _verify_args(target, q, toks, u, temperature, B, n, V)
+        self.args.accepted = self.accepted.data_ptr()
+        self.args.token = self.token.data_ptr()
+        self._ws = L.workspace(dev, L.lib().wh_verify_workspace_bytes(B, n, V))
+        self.args.workspace = self._ws.data_ptr()
+        self.args.workspace_bytes = self._ws.numel()
+        self._alive = (target, q, toks, u)
+        self._stream = ctypes.c_void_p(L.stream_of(target))
+        self._fn = L.lib().wh_verify_fused
+        self._ref = ctypes.byref(self.args)
+
+    def __call__(self):
+        L.check(self._fn(self._ref, self._stream))
+        return self.accepted, self.token
+
+
 def exp_fix44(d: torch.Tensor) -> torch.Tensor:
     """Device contract exponential floor(2^44 exp(d)) as int64 (test hook)."""
     d = d.float().contiguous()

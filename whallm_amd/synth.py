@@ -94,6 +94,13 @@ class VerifyWorkload:
     uniforms: np.ndarray       # [B, n+1]
     temperature: float
 
+    def bytes_per_call(self) -> int:
+        """Algorithmic bytes: target logits and draft probabilities of every
+        position, draft ids and uniforms read once; accepted count and token
+        written once."""
+        B, n, V = self.B, self.n, self.V
+        return B * (n + 1) * V * 4 + B * n * V * 4 + B * n * 4 + B * (n + 1) * 4 + B * 8
+
 
 def _rngs(idx: int):
     return np.random.Generator(np.random.PCG64(SEED0 + idx)), np.random.Generator(np.random.PCG64(SEED0 + idx + 1000))
