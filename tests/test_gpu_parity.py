@@ -282,6 +282,47 @@ def test_verify_fused_workload3_full_size(S, dev, oracle):
     assert np.array_equal(t.cpu().numpy(), ot)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("force_exact", [False, True])
+@pytest.mark.parametrize("seed", range(10))
+def test_verify_fused_sliced(S, dev, oracle, seed, force_exact, monkeypatch):
+    """The sliced verifier (T > 0, V % 4 == 0): bounds-decided ratio tests,
+    exact residual draw; with WH_VERIFY_FORCE_EXACT every entry takes the
+    exact per-row algorithm that undecided entries use."""
+    rng = np.random.default_rng(700 + seed)
+    B, n = int(rng.integers(1, 20)), int(rng.integers(1, 11))
+    V = int(rng.choice([4096, 20000, 129280])) if seed < 8 else 129280
+    T = float(rng.choice([0.3, 0.8, 1.0, 2.0]))
+    x = rng.normal(0, 2.5, (B, n + 1, V)).astype(np.float32)
+    if seed % 4 == 1:
+        x = (np.round(x * 4) / 4).astype(np.float32)  # dense ties
+    dl = x[:, :n].astype(np.float64) + rng.normal(0, 0.5, (B, n, V))
+    z = dl / T
+    z -= z.max(-1, keepdims=True)
+    q = np.exp(z)
+    q /= q.sum(-1, keepdims=True)
+    cdf = np.cumsum(q, -1)
+    toks = np.array([[min(int(np.searchsorted(cdf[b, j], rng.random() * cdf[b, j, -1], side="right")), V - 1)
+                      for j in range(n)] for b in range(B)], np.int32)
+    q = q.astype(np.float32)
+    if seed % 4 == 2:
+        x[rng.random(x.shape) < 0.3] = -np.inf
+        x[0, 0, :] = -np.inf  # a row with no finite logit
+    if seed % 4 == 3:
+        q[rng.random(q.shape) < 0.1] = 0.0
+    if seed % 5 == 0:
+        toks[0, 0] = V  # out of range: rejected
+    u = rng.random((B, n + 1), dtype=np.float32)
+    if force_exact:
+        monkeypatch.setenv("WH_VERIFY_FORCE_EXACT", "1")
+    oa, ot = oracle.verify_fused(x, q, toks, u, T)
+    announce(f"wh_verify_fused sliced seed={seed} B={B} n={n} V={V} T={T} force_exact={force_exact}")
+    a, t = S.verify_fused(torch.from_numpy(x).to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(toks).to(dev),
+                          T, uniforms=torch.from_numpy(u).to(dev))
+    assert np.array_equal(a.cpu().numpy(), oa)
+    assert np.array_equal(t.cpu().numpy(), ot)
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_verify_fused_random(S, dev, oracle, seed):
     rng = np.random.default_rng(600 + seed)

@@ -16,6 +16,7 @@
 // All decisions are exact: masses are floor(2^44 exp(.)) integers, the
 // ratio test u*q*Z > W is evaluated in 128-bit integers.
 #include <cmath>
+#include <cstdlib>
 
 #include "wh_common.h"
 #include "wh_internal.h"
@@ -41,6 +42,7 @@ struct VerifyKArgs {
 
 struct VSmem {
   uint64_t scratch64[16];
+  double scratchd[16];
   float scratchf[16];
   int scratchi[16];
   int bcasti[4];
@@ -273,6 +275,411 @@ __global__ void __launch_bounds__(1024) verify_fused_draw_kernel(VerifyKArgs a) 
   if (tid == 0) { a.accepted[b] = j; a.token[b] = tok; }
 }
 
+// ---------------------------------------------------------------------------
+// Fused form, T > 0: sliced passes instead of one workgroup per row.
+//   1. verify_sum_kernel, one 512-thread workgroup per slice of every target
+//      row (several per CU): the slice's exact max and a float sum of
+//      exp((x - max) / T), streamed with a running max.  One HBM pass over
+//      the target rows.
+//   2. verify_prep_kernel, G2 workgroups per batch entry: each recomputes the
+//      accept / reject decisions from the row summaries -- the normaliser Z
+//      lies in [Zlo, Zhi] from the float sums, and u q Z > W is decided from
+//      both ends (W exact, from the draft token's logit); the first
+//      rejection j* is settled unless a test falls between them -- then sums
+//      the exact fixed-point weights of its slice of row j*.
+//   3. verify_resid_kernel: with the exact Z of row j*, the slice's residual
+//      mass sum max(W_i - floor(q_i Z), 0).
+//   4. verify_pick_kernel, one workgroup per batch entry: the slice holding
+//      the draw target, then the element inside it.  A batch entry whose
+//      decisions were not settled by the bounds runs the exact per-row
+//      algorithm here instead (identical results, slower).
+// ---------------------------------------------------------------------------
+constexpr int VT1 = 512;       // threads, pass 1
+constexpr int VE1 = 32768;     // elements per pass-1 slice, at most
+constexpr int VT2 = 1024;      // threads, passes 2 and 3
+constexpr int VG2MAX = 16;     // slices of the selected row
+constexpr int VSEG4 = 2;       // float4 groups per thread in the final draw (1024 threads: 8192 ids)
+constexpr double VEPS = 2e-4;  // relative slack of the float normaliser
+
+struct VRowSum {
+  float m;
+  float pad;
+  double zf;  // sum of exp((x - m) / T) over the slice (hardware exp)
+};
+
+struct VPlan {
+  int G1, SL1, G2, SL2;
+  int force_exact;  // test hook: every batch entry takes the exact per-row algorithm
+  VRowSum* summ;  // [B, n+1, G1]
+  int32_t* jst;   // [B, 2]: j*, undecided flag
+  unsigned long long* zpart;  // [B, G2] exact weights of row j*
+  unsigned long long* rpart;  // [B, G2] residual mass of row j*
+};
+
+__device__ __forceinline__ float vweight_arg(float x, float m, float Tc) { return (x - m) / Tc; }
+
+__global__ void __launch_bounds__(VT1) verify_sum_kernel(VerifyKArgs a, VPlan P) {
+  __shared__ VSmem sm;
+  const int tid = threadIdx.x;
+  const int rj = blockIdx.x / P.G1, s = blockIdx.x - rj * P.G1;
+  const int V = a.V;
+  const int v0 = s * P.SL1, v1 = min(V, v0 + P.SL1);
+  const float* row = a.target + (long long)rj * V;
+  const float iT = 1.0f / a.Tc;
+  // per thread: a running max and the float sum of exp((x - max) / T),
+  // rescaled whenever the max rises
+  float mt = -INFINITY, st = 0.0f;
+#pragma unroll 4
+  for (int i = v0 + tid * 4; i < v1; i += VT1 * 4) {
+    const float4 c = *(const float4*)(row + i);
+    const float cm = fmaxf(fmaxf(c.x, c.y), fmaxf(c.z, c.w));
+    if (cm > mt) {
+      st = mt == -INFINITY ? 0.0f : st * __expf((mt - cm) * iT);
+      mt = cm;
+    }
+    if (mt != -INFINITY) {
+      st += __expf((c.x - mt) * iT) + __expf((c.y - mt) * iT);
+      st += __expf((c.z - mt) * iT) + __expf((c.w - mt) * iT);
+    }
+  }
+  const float m = block_reduce(mt, sm.scratchf, OpMaxF(), -INFINITY);
+  const double zt = mt == -INFINITY ? 0.0 : (double)st * (double)__expf((mt - m) * iT);
+  const double zs = block_reduce(zt, sm.scratchd, OpSumF64(), 0.0);
+  if (tid == 0) {
+    VRowSum o;
+    o.m = m;
+    o.pad = 0.0f;
+    o.zf = zs;
+    P.summ[blockIdx.x] = o;
+  }
+}
+
+// Row j of batch entry b from the slice summaries: the max, and the proven
+// interval of the fixed-point normaliser.
+__device__ void vrow_bounds(const VerifyKArgs& a, const VPlan& P, int b, int j, float* m_out, uint64_t* zlo,
+                            uint64_t* zhi) {
+  const VRowSum* rs = P.summ + ((long long)b * (a.n + 1) + j) * P.G1;
+  float m = -INFINITY;
+  for (int s = 0; s < P.G1; ++s) m = fmaxf(m, rs[s].m);
+  // the float rescale's relative error (a few ulp) is far inside VEPS
+  double zf = 0.0;
+  if (m != -INFINITY)
+    for (int s = 0; s < P.G1; ++s)
+      if (rs[s].m != -INFINITY) zf += rs[s].zf * (double)__expf((rs[s].m - m) / a.Tc);
+  const double SC = 17592186044416.0, LIM = 4.0e18;
+  const double lo = zf * SC * (1.0 - VEPS) - (double)a.V, hi = zf * SC * (1.0 + VEPS) + (double)a.V;
+  *m_out = m;
+  *zlo = (m == -INFINITY || lo <= 0.0) ? 0ull : (uint64_t)lo;
+  *zhi = m == -INFINITY ? 0ull : (hi >= LIM ? (1ull << 62) : (uint64_t)ceil(hi));
+}
+
+// Row j's max from the slice summaries.
+__device__ __forceinline__ float vrow_max(const VerifyKArgs& a, const VPlan& P, int b, int j) {
+  const VRowSum* rs = P.summ + ((long long)b * (a.n + 1) + j) * P.G1;
+  float m = -INFINITY;
+  for (int s = 0; s < P.G1; ++s) m = fmaxf(m, rs[s].m);
+  return m;
+}
+
+__global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P) {
+  __shared__ VSmem sm;
+  __shared__ int s_state[64];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x / P.G2, s = blockIdx.x - b * P.G2;
+  const int n = a.n, V = a.V;
+  // decisions: 0 accept, 1 reject, 2 undecided by the bounds
+  if (tid < n) {
+    const int j = tid;
+    const int tk = a.tok[(long long)b * n + j];
+    float m;
+    uint64_t zlo, zhi;
+    vrow_bounds(a, P, b, j, &m, &zlo, &zhi);
+    int st;
+    if (tk < 0 || tk >= V) {
+      st = 1;
+    } else {
+      const float xt = a.target[((long long)b * (n + 1) + j) * V + tk];
+      const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(xt, m, a.Tc));
+      const float q = a.draft[((long long)b * n + j) * V + tk];
+      const float u = a.u[(long long)b * (n + 1) + j];
+      if (reject_fused(u, q, zlo, W)) st = 1;
+      else if (!reject_fused(u, q, zhi, W)) st = 0;
+      else st = 2;
+    }
+    s_state[j] = st;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int j = 0, und = 0;
+    for (; j < n; ++j) {
+      if (s_state[j] == 0) continue;
+      if (s_state[j] == 2) und = 1;
+      break;
+    }
+    if (P.force_exact) und = 1;
+    sm.bcasti[0] = j;
+    sm.bcasti[1] = und;
+    if (s == 0) {
+      P.jst[2 * b] = j;
+      P.jst[2 * b + 1] = und;
+    }
+  }
+  __syncthreads();
+  const int js = sm.bcasti[0];
+  if (sm.bcasti[1]) return;
+  const float m = vrow_max(a, P, b, js);
+  const float* x = a.target + ((long long)b * (n + 1) + js) * V;
+  const int v0 = s * P.SL2, v1 = min(V, v0 + P.SL2);
+  uint64_t z = 0;
+  if (m != -INFINITY)
+#pragma unroll 4
+    for (int i = v0 + tid * 4; i < v1; i += VT2 * 4) {
+      const float4 c = *(const float4*)(x + i);
+      z += exp_fix44(vweight_arg(c.x, m, a.Tc)) + exp_fix44(vweight_arg(c.y, m, a.Tc));
+      z += exp_fix44(vweight_arg(c.z, m, a.Tc)) + exp_fix44(vweight_arg(c.w, m, a.Tc));
+    }
+  const uint64_t zt = block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
+  if (tid == 0) P.zpart[(long long)b * P.G2 + s] = zt;
+}
+
+__global__ void __launch_bounds__(VT2) verify_resid_kernel(VerifyKArgs a, VPlan P) {
+  __shared__ VSmem sm;
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x / P.G2, s = blockIdx.x - b * P.G2;
+  const int n = a.n, V = a.V;
+  const int js = P.jst[2 * b];
+  if (P.jst[2 * b + 1] || js >= n) return;
+  uint64_t Z = 0;
+  for (int t = 0; t < P.G2; ++t) Z += P.zpart[(long long)b * P.G2 + t];
+  const float m = vrow_max(a, P, b, js);
+  const float* x = a.target + ((long long)b * (n + 1) + js) * V;
+  const float* q = a.draft + ((long long)b * n + js) * V;
+  const int v0 = s * P.SL2, v1 = min(V, v0 + P.SL2);
+  uint64_t r = 0;
+  auto res = [&](float xv, float qv) {
+    const uint64_t w = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(xv, m, a.Tc));
+    const uint64_t qz = floor_qz(qv, Z);
+    return w > qz ? w - qz : (uint64_t)0;
+  };
+#pragma unroll 4
+  for (int i = v0 + tid * 4; i < v1; i += VT2 * 4) {
+    const float4 c = *(const float4*)(x + i);
+    const float4 d = *(const float4*)(q + i);
+    r += res(c.x, d.x) + res(c.y, d.y) + res(c.z, d.z) + res(c.w, d.w);
+  }
+  const uint64_t rt = block_reduce(r, sm.scratch64, OpSumU64(), (uint64_t)0);
+  if (tid == 0) P.rpart[(long long)b * P.G2 + s] = rt;
+}
+
+// The first index in [lo, hi) whose inclusive weight sum exceeds rem (the
+// weights there sum to more than rem).  Thread t owns the contiguous segment
+// [lo + 4 SEG4 t, lo + 4 SEG4 (t + 1)); its weights are computed once, from
+// float4 loads issued together, and kept in registers for both passes.
+// Requires hi - lo <= 4 * SEG4 * blockDim.x and lo % 4 == hi % 4 == 0.
+template <int SEG4, typename WF>
+__device__ int segment_find(int lo, int hi, uint64_t rem, const float* x, const float* q, WF w, VSmem& sm) {
+  const int tid = threadIdx.x;
+  const int a0 = lo + tid * 4 * SEG4;
+  float4 cx[SEG4], cq[SEG4];
+#pragma unroll
+  for (int k = 0; k < SEG4; ++k) {
+    const int i = a0 + 4 * k;
+    const int ic = i < hi ? i : lo;
+    cx[k] = *(const float4*)(x + ic);
+    cq[k] = q ? *(const float4*)(q + ic) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  uint64_t wv[4 * SEG4];
+  uint64_t sum = 0;
+#pragma unroll
+  for (int e = 0; e < 4 * SEG4; ++e) wv[e] = 0ull;
+  if (a0 < hi) {  // whole waves past the slice skip the weights
+#pragma unroll
+    for (int k = 0; k < SEG4; ++k) {
+      const bool in = a0 + 4 * k < hi;
+      wv[4 * k] = in ? w(cx[k].x, cq[k].x) : 0ull;
+      wv[4 * k + 1] = in ? w(cx[k].y, cq[k].y) : 0ull;
+      wv[4 * k + 2] = in ? w(cx[k].z, cq[k].z) : 0ull;
+      wv[4 * k + 3] = in ? w(cx[k].w, cq[k].w) : 0ull;
+      sum += wv[4 * k] + wv[4 * k + 1] + wv[4 * k + 2] + wv[4 * k + 3];
+    }
+  }
+  uint64_t tot;
+  const uint64_t excl = block_exclusive_scan_u64(sum, sm.scratch64, &tot);
+  if (tid == 0) sm.bcasti[2] = lo;
+  __syncthreads();
+  if (excl <= rem && rem < excl + sum) {
+    uint64_t c = excl;
+    int hit = -1;
+#pragma unroll
+    for (int e = 0; e < 4 * SEG4; ++e) {
+      c += wv[e];
+      if (hit < 0 && c > rem) hit = e;
+    }
+    sm.bcasti[2] = a0 + hit;
+  }
+  __syncthreads();
+  return sm.bcasti[2];
+}
+
+// The exact per-row algorithm for batch entry b by one workgroup: every
+// row's max and normaliser by block reductions, the tests in order, then the
+// residual (or bonus) draw over the whole row.
+__device__ void verify_exact_entry(const VerifyKArgs& a, int b, VSmem& sm) {
+  const int tid = threadIdx.x, n = a.n, V = a.V;
+  int j = 0;
+  float m = -INFINITY;
+  uint64_t Z = 0;
+  for (; j <= n; ++j) {
+    const float* x = a.target + ((long long)b * (n + 1) + j) * V;
+    m = block_max(x, V, sm);
+    uint64_t z = 0;
+    if (m != -INFINITY)
+      for (int i = tid; i < V; i += blockDim.x) z += exp_fix44(vweight_arg(x[i], m, a.Tc));
+    Z = block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
+    if (j == n) break;
+    const int tk = a.tok[(long long)b * n + j];
+    bool rj;
+    if (tk < 0 || tk >= V) {
+      rj = true;
+    } else {
+      const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(x[tk], m, a.Tc));
+      rj = reject_fused(a.u[(long long)b * (n + 1) + j], a.draft[((long long)b * n + j) * V + tk], Z, W);
+    }
+    if (rj) break;
+  }
+  const float* x = a.target + ((long long)b * (n + 1) + j) * V;
+  const float u = a.u[(long long)b * (n + 1) + n];
+  auto wt = [&](int i) { return m == -INFINITY ? (uint64_t)0 : exp_fix44(vweight_arg(x[i], m, a.Tc)); };
+  int tok = 0;
+  uint64_t tot;
+  if (j == n) {
+    tok = Z ? segment_draw(V, u, wt, sm, &tot) : 0;
+  } else {
+    const float* q = a.draft + ((long long)b * n + j) * V;
+    auto resid = [&](int i) {
+      const uint64_t w = wt(i), qz = floor_qz(q[i], Z);
+      return w > qz ? w - qz : (uint64_t)0;
+    };
+    uint64_t S;
+    tok = segment_draw(V, u, resid, sm, &S);
+    if (S == 0) tok = Z ? segment_draw(V, u, wt, sm, &tot) : 0;
+  }
+  if (tid == 0) {
+    a.accepted[b] = j;
+    a.token[b] = tok;
+  }
+}
+
+__global__ void __launch_bounds__(1024) verify_pick_kernel(VerifyKArgs a, VPlan P) {
+  __shared__ VSmem sm;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int n = a.n, V = a.V;
+  const int js = P.jst[2 * b];
+  if (P.jst[2 * b + 1]) {
+    verify_exact_entry(a, b, sm);
+    return;
+  }
+  uint64_t Z = 0, R = 0;
+  for (int t = 0; t < P.G2; ++t) {
+    Z += P.zpart[(long long)b * P.G2 + t];
+    if (js < n) R += P.rpart[(long long)b * P.G2 + t];
+  }
+  // residual mass when rejected and positive, else the row's own weights
+  const bool use_r = js < n && R > 0;
+  const unsigned long long* parts = (use_r ? P.rpart : P.zpart) + (long long)b * P.G2;
+  const uint64_t total = use_r ? R : Z;
+  int tok = 0;
+  if (total) {
+    const uint64_t tgt = draw_target(a.u[(long long)b * (n + 1) + n], total);
+    uint64_t before = 0;
+    int ss = P.G2 - 1;
+    for (int t = 0; t < P.G2; ++t) {
+      if (before + parts[t] > tgt) {
+        ss = t;
+        break;
+      }
+      before += parts[t];
+    }
+    const uint64_t rem = tgt - before;
+    const float m = vrow_max(a, P, b, js);
+    const float* x = a.target + ((long long)b * (n + 1) + js) * V;
+    const int v0 = ss * P.SL2, v1 = min(V, v0 + P.SL2);
+    auto wt = [&](float xv) { return m == -INFINITY ? (uint64_t)0 : exp_fix44(vweight_arg(xv, m, a.Tc)); };
+    if (use_r) {
+      const float* q = a.draft + ((long long)b * n + js) * V;
+      tok = segment_find<VSEG4>(v0, v1, rem, x, q, [&](float xv, float qv) {
+        const uint64_t w = wt(xv), qz = floor_qz(qv, Z);
+        return w > qz ? w - qz : (uint64_t)0;
+      }, sm);
+    } else {
+      tok = segment_find<VSEG4>(v0, v1, rem, x, nullptr, [&](float xv, float) { return wt(xv); }, sm);
+    }
+  }
+  if (tid == 0) {
+    a.accepted[b] = js;
+    a.token[b] = tok;
+  }
+}
+
+struct VHostPlan {
+  int G1, SL1, G2, SL2;
+  size_t summ, jst, zpart, rpart, total;
+};
+
+// Workspace: the per-position slots of the one-workgroup-per-row form, then
+// the sliced form's row summaries and per-entry sums.
+static VHostPlan vplan(int B, int n, int V) {
+  VHostPlan h;
+  h.G1 = std::max(1, (V + VE1 - 1) / VE1);
+  h.SL1 = ((V + h.G1 - 1) / h.G1 + 3) / 4 * 4;
+  h.G2 = std::max(1, std::min(VG2MAX, (256 + std::max(B, 1) - 1) / std::max(B, 1)));
+  // a slice of the selected row must fit the final draw's register segments
+  h.G2 = std::max(h.G2, (V + 4 * VSEG4 * 1024 - 1) / (4 * VSEG4 * 1024));
+  h.SL2 = ((V + h.G2 - 1) / h.G2 + 3) / 4 * 4;
+  const size_t slots = (size_t)std::max(B, 0) * (size_t)std::max(n, 0);
+  size_t off = (slots * 16 + 255) / 256 * 256;
+  h.summ = off;
+  off += (size_t)std::max(B, 0) * (std::max(n, 0) + 1) * h.G1 * sizeof(VRowSum);
+  h.jst = off;
+  off += (size_t)std::max(B, 0) * 8;
+  off = (off + 15) / 16 * 16;
+  h.zpart = off;
+  off += (size_t)std::max(B, 0) * h.G2 * 8;
+  h.rpart = off;
+  off += (size_t)std::max(B, 0) * h.G2 * 8;
+  h.total = off + 256;
+  return h;
+}
+
+static int launch_verify_sliced(const VerifyKArgs& k, const VHostPlan& h, char* ws, hipStream_t st) {
+  VPlan P;
+  // WH_VERIFY_FORCE_EXACT=1 (tests only) routes every batch entry through the
+  // exact per-row algorithm that entries undecided by the bounds take
+  const char* fe = getenv("WH_VERIFY_FORCE_EXACT");
+  P.force_exact = (fe && fe[0] == '1') ? 1 : 0;
+  P.G1 = h.G1;
+  P.SL1 = h.SL1;
+  P.G2 = h.G2;
+  P.SL2 = h.SL2;
+  P.summ = (VRowSum*)(ws + h.summ);
+  P.jst = (int32_t*)(ws + h.jst);
+  P.zpart = (unsigned long long*)(ws + h.zpart);
+  P.rpart = (unsigned long long*)(ws + h.rpart);
+  hipLaunchKernelGGL(verify_sum_kernel, dim3(k.B * (k.n + 1) * h.G1), dim3(VT1), 0, st, k, P);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(WH_EHIP, "verify_sum_kernel launch failed: %s", hipGetErrorString(e));
+  hipLaunchKernelGGL(verify_prep_kernel, dim3(k.B * h.G2), dim3(VT2), 0, st, k, P);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(WH_EHIP, "verify_prep_kernel launch failed: %s", hipGetErrorString(e));
+  hipLaunchKernelGGL(verify_resid_kernel, dim3(k.B * h.G2), dim3(VT2), 0, st, k, P);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(WH_EHIP, "verify_resid_kernel launch failed: %s", hipGetErrorString(e));
+  hipLaunchKernelGGL(verify_pick_kernel, dim3(k.B), dim3(1024), 0, st, k, P);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(WH_EHIP, "verify_pick_kernel launch failed: %s", hipGetErrorString(e));
+  return WH_OK;
+}
+
 static int check_verify(const wh_verify_args* p, bool fused) {
   if (!p) return fail(WH_EINVAL, "args is NULL");
   if (p->B < 0 || p->n < 0) return fail(WH_EINVAL, "B and n must be >= 0");
@@ -309,9 +716,7 @@ static VerifyKArgs to_kargs(const wh_verify_args* p) {
 using namespace wh;
 
 extern "C" size_t wh_verify_workspace_bytes(int32_t B, int32_t n, int32_t V) {
-  (void)V;
-  size_t slots = (size_t)(B > 0 ? B : 0) * (size_t)(n > 0 ? n : 0);
-  return slots * 16 + 256;
+  return vplan(B, n, V > 0 ? V : 1).total;
 }
 
 extern "C" int wh_verify_logprobs(const wh_verify_args* args, void* stream) {
@@ -337,6 +742,12 @@ extern "C" int wh_verify_fused(const wh_verify_args* args, void* stream) {
   VerifyKArgs k = to_kargs(args);
   size_t slots = (size_t)args->B * args->n;
   char* ws = (char*)args->workspace;
+  hipStream_t st0 = (hipStream_t)stream;
+  // the sliced passes need 16-byte aligned rows (float4 loads) and n < 64
+  const VHostPlan vh = vplan(args->B, args->n, args->V);
+  const bool sliced = args->temperature > 0.0f && args->n > 0 && args->n < 64 && args->V % 4 == 0 &&
+                      (uintptr_t)args->target % 16 == 0 && (uintptr_t)args->draft % 16 == 0 && ws;
+  if (sliced) return launch_verify_sliced(k, vh, ws, st0);
   k.rz = (unsigned long long*)ws;
   k.rmax = (float*)(ws + slots * 8);
   k.rej = (int32_t*)(ws + slots * 12);
