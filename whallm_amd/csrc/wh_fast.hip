@@ -390,12 +390,11 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   const int32_t* hrow = a.hist + (long long)b * a.hist_stride;
   if (pen) {
     if (pf) {
-      // the addresses do not wait for the length (a scalar load still in
-      // flight while the logits loads issue)
+      // the addresses do not need the length, which is read after the
+      // logits loads have issued
 #pragma unroll
       for (int q = 0; q < HPF; ++q)
         if (q * FT < hs) hreg[q] = hrow[min(tid + q * FT, hs - 1)];
-      len = max(0, min(*(cint*)(a.hist_len + b), hs));
     } else {
       // rows longer than the prefetch read the last HPF * FT positions
       // (every window is a suffix of at most WH_MAX_WINDOW ids)
@@ -413,6 +412,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     d[r] = *(const uint4*)(rowp + (size_t)(g < v1 ? g : v0) * ESZ);
   }
   asm volatile("" ::: "memory");
+  if (pen && pf) len = max(0, min(*(cint*)(a.hist_len + b), hs));
   const RowParams rp = row_params(a, raw, P.rule_cap);
   SliceHdr* hdr = P.hdr + (long long)b * P.G + s;
   if (rp.all) {
