@@ -44,21 +44,36 @@ __device__ __forceinline__ uint64_t exp_fix44(float d) {
   return flush ? 0ull : r;
 }
 
+// 16-byte load of a once-read stream (logits), marked non-temporal: the
+// stream then does not displace what the caches hold for the next kernel
+// (its code and the workspace lines it reads).
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // float32 mantissa/exponent split: x = M * 2^(e - 24), M a 24-bit integer.
 __device__ __forceinline__ uint64_t mant24(float x, int* e) {
   float fr = frexpf(x, e);
   return (uint64_t)ldexpf(fr, 24);
 }
 
-// floor(theta * Z) for float32 theta in [0,1), Z < 2^62 (exact).
+// floor(theta * Z) for float32 theta in [0,1), Z < 2^62 (exact).  theta =
+// M 2^-s with a 24-bit M and s >= 23, so with Z = Zh 2^32 + Zl the product
+// M Z = hi 2^32 + lo (hi = M Zh < 2^54, lo = M Zl < 2^56) is shifted in two
+// 64-bit pieces: for s <= 32, hi 2^(32-s) is whole and only lo loses bits;
+// beyond, (M Z) >> 32 = hi + (lo >> 32).
 __device__ __forceinline__ uint64_t floor_theta_z(float theta, uint64_t Z) {
   if (!(theta > 0.0f)) return 0;
   if (theta > 1.0f) theta = 1.0f;
   int e;
-  uint64_t M = mant24(theta, &e);
-  int s = 24 - e;
-  u128 prod = (u128)M * (u128)Z;
-  return s >= 128 ? 0 : (uint64_t)(prod >> s);
+  const uint64_t M = mant24(theta, &e);
+  const int s = 24 - e;
+  const uint64_t lo = M * (Z & 0xFFFFFFFFull), hi = M * (Z >> 32);
+  if (s <= 32) return (hi << (32 - s)) + (lo >> s);
+  const uint64_t t = hi + (lo >> 32);
+  return s - 32 >= 64 ? 0 : t >> (s - 32);
 }
 
 // u in [0,1) -> floor(u * 2^32), clamped; NaN and negatives give 0.
@@ -68,9 +83,11 @@ __device__ __forceinline__ uint64_t u32_fix(float u) {
   return (uint64_t)(u * 4294967296.0f);
 }
 
-// Draw target inside a total weight: floor(U * total / 2^32).
+// Draw target inside a total weight: floor(U * total / 2^32), total < 2^62,
+// as U Th + ((U Tl) >> 32) with total = Th 2^32 + Tl (exact: U Th is whole).
 __device__ __forceinline__ uint64_t draw_target(float u, uint64_t total) {
-  return (uint64_t)(((u128)u32_fix(u) * (u128)total) >> 32);
+  const uint64_t U = u32_fix(u);
+  return U * (total >> 32) + ((U * (total & 0xFFFFFFFFull)) >> 32);
 }
 
 // Monotone 32-bit key of a float (larger value -> larger key); callers map
@@ -239,6 +256,24 @@ __device__ __forceinline__ uint32_t wscan_incl_u32(uint32_t x) {
   x += dpp32z<0x142, 0xA>(x);
   x += dpp32z<0x143, 0xC>(x);
   return x;
+}
+
+// K independent inclusive scans interleaved (as wsum_u64_k): lane 63 ends
+// with each total.
+template <int K>
+__device__ __forceinline__ void wscan_incl_u64_k(uint64_t (&v)[K]) {
+#define WH_SCANK_STEP(C, ROWS)                                                                              \
+  _Pragma("unroll") for (int k_ = 0; k_ < K; ++k_) {                                                        \
+    const uint64_t y_ = ((uint64_t)dpp32z<C, ROWS>((uint32_t)(v[k_] >> 32)) << 32) | dpp32z<C, ROWS>((uint32_t)v[k_]); \
+    v[k_] += y_;                                                                                            \
+  }
+  WH_SCANK_STEP(0x111, 0xF)
+  WH_SCANK_STEP(0x112, 0xF)
+  WH_SCANK_STEP(0x114, 0xF)
+  WH_SCANK_STEP(0x118, 0xF)
+  WH_SCANK_STEP(0x142, 0xA)
+  WH_SCANK_STEP(0x143, 0xC)
+#undef WH_SCANK_STEP
 }
 
 // Number of lanes (of the active ones) where p holds; wave uniform.

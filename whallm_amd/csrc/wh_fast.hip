@@ -34,10 +34,11 @@
 //   * When the top-p cut needs the normaliser closely, a hardware-exp float
 //     sum over the slice.
 //
-// merge_kernel: one workgroup per row.  Wave 0 loads the G summaries and the
-// first QSPEC 64-candidate chunks of the row (chunk t / G of slice t % G) in
-// one round trip.  It keeps up to 16 candidates per lane in registers and runs
-// the integer contract over them:
+// merge_kernel: one workgroup per row.  Each of its eight waves loads the G
+// summaries and QW of the row's first QSPEC 64-candidate chunks (chunk t / G
+// of slice t % G) in one round trip, computes their exact masses and appends
+// the candidates that can still be kept to one LDS list.  Wave 0 then keeps
+// up to 16 of them per lane in registers and runs the integer contract:
 //   * the proven interval [Zlo, Zhi] for the normaliser;
 //   * top-k / top-p / min-p in the chain's order;
 //   * the inverse-CDF draw, a 6-bit radix descent over the id.
@@ -60,7 +61,9 @@ constexpr int FAST_CAP = 2048;    // candidate capacity per slice
 constexpr int RUNGS = 8;          // thresholds per ladder round
 constexpr int LADDER_ROUNDS = 5;  // ladder rounds at most (the first, a far one, refinements)
 constexpr int QM = 16;            // merge: candidate slots per lane, at most
-constexpr int QSPEC = 16;         // merge: slots loaded speculatively with the summaries (slices <= 16)
+constexpr int MW = 8;             // merge: waves per workgroup
+constexpr int QW = 2;             // merge: candidate chunks each wave loads with the summaries
+constexpr int QSPEC = MW * QW;    // merge: chunks loaded speculatively per row
 constexpr int HDR_OVERFLOW = 1;   // SliceHdr.flags: the row needs the exact engine
 constexpr float BAND1 = 1.5f;     // band floors below tau, nats
 constexpr float BAND2 = 3.5f;
@@ -409,7 +412,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int g = v0 + (r * FT + tid) * EPT;
-    d[r] = *(const uint4*)(rowp + (size_t)(g < v1 ? g : v0) * ESZ);
+    d[r] = load_stream16(rowp + (size_t)(g < v1 ? g : v0) * ESZ);
   }
   asm volatile("" ::: "memory");
   if (pen && pf) len = max(0, min(*(cint*)(a.hist_len + b), hs));
@@ -724,7 +727,7 @@ struct ZBounds {
 };
 
 // [Zlo, Zhi] for Z = sum_i exp_fix44(l_i - m) over the row, from the slice
-// summaries (lane s < G holds slice s) and the exact candidate mass Scand.
+// summaries and the exact candidate mass Scand.
 //  * Lower bound: the candidates' exact masses, plus for every group counted
 //    in a band [t_j, t_(j-1)) at least one element of mass
 //    >= floor(2^44 e^(t_j - m) (1 - eps)) - 1.
@@ -732,48 +735,62 @@ struct ZBounds {
 //  * When every slice carries its float sum zf (hardware exp, relative error
 //    far below eps = 2e-4 for every term that exp_fix44 does not flush to 0),
 //    both bounds are also taken from zf.
-template <int G>
-__device__ __forceinline__ ZBounds z_bounds(const SliceHdr& hd, bool own, float m, uint64_t Scand) {
+// The summaries' share (ZParts, summed over the slices in slice order) does
+// not depend on the candidates, so it is computed beside them.
+struct ZParts {
+  double lo, hi, zl, zh;
+  int nz;  // slices without a float sum
+};
+
+__device__ __forceinline__ ZParts z_slice(const SliceHdr& h, float m) {
   const double SC = 17592186044416.0, EPS = 2e-4;
-  double lo = 0.0, hi = 0.0, zl = 0.0, zh = 0.0;
-  int no_zf = 0;
-  if (own && hd.m != -INFINITY) {
-    // float exponentials: their error (a few ulp, arguments <= 0) is far
-    // inside EPS
-    auto wlo = [&](float t) {
-      return t == -INFINITY ? 0.0 : fmax(floor((double)expf(t - m) * SC * (1.0 - EPS)) - 1.0, 0.0);
-    };
-    lo = (double)hd.g1 * wlo(hd.t1) + (double)hd.g2 * wlo(hd.t2);
-    hi = (double)(hd.nall - hd.n) * ((double)expf(hd.tau - m) * SC * (1.0 + EPS) + 1.0);
-    if (hd.zf >= 0.0) {
-      const double sc = (double)expf(hd.m - m) * SC;
-      zl = hd.zf * sc * (1.0 - EPS) - (double)hd.nall;
-      zh = hd.zf * sc * (1.0 + EPS) + (double)hd.nall;
-    } else {
-      no_zf = 1;
-    }
+  ZParts p{0.0, 0.0, 0.0, 0.0, 0};
+  if (h.m == -INFINITY) return p;
+  // float exponentials: their error (a few ulp, arguments <= 0) is far inside
+  // EPS
+  auto wlo = [&](float t) {
+    return t == -INFINITY ? 0.0 : fmax(floor((double)expf(t - m) * SC * (1.0 - EPS)) - 1.0, 0.0);
+  };
+  p.lo = (double)h.g1 * wlo(h.t1) + (double)h.g2 * wlo(h.t2);
+  p.hi = (double)(h.nall - h.n) * ((double)expf(h.tau - m) * SC * (1.0 + EPS) + 1.0);
+  if (h.zf >= 0.0) {
+    const double sc = (double)expf(h.m - m) * SC;
+    p.zl = h.zf * sc * (1.0 - EPS) - (double)h.nall;
+    p.zh = h.zf * sc * (1.0 + EPS) + (double)h.nall;
+  } else {
+    p.nz = 1;
   }
-  // lanes 0..G-1 hold the slices: read them directly
+  return p;
+}
+
+// Lanes 0..G-1 hold the slices: each takes its own share, and the G shares
+// are read across the lanes.
+template <int G>
+__device__ __forceinline__ ZParts z_parts(const SliceHdr& hd, bool own, float m) {
+  const ZParts q = own ? z_slice(hd, m) : ZParts{0.0, 0.0, 0.0, 0.0, 0};
   auto lane_f64 = [](double v, int l) {
     return __longlong_as_double((long long)lane_u64((uint64_t)__double_as_longlong(v), l));
   };
-  double slo = 0.0, shi = 0.0, szl = 0.0, szh = 0.0;
-  int nz = 0;
+  ZParts s{0.0, 0.0, 0.0, 0.0, 0};
 #pragma unroll
   for (int l = 0; l < G; ++l) {
-    slo += lane_f64(lo, l);
-    shi += lane_f64(hi, l);
-    szl += lane_f64(zl, l);
-    szh += lane_f64(zh, l);
-    nz += (int)lane_u32((uint32_t)no_zf, l);
+    s.lo += lane_f64(q.lo, l);
+    s.hi += lane_f64(q.hi, l);
+    s.zl += lane_f64(q.zl, l);
+    s.zh += lane_f64(q.zh, l);
+    s.nz += (int)lane_u32((uint32_t)q.nz, l);
   }
+  return s;
+}
+
+__device__ __forceinline__ ZBounds z_finish(const ZParts& s, uint64_t Scand) {
   const double LIM = 4.0e18;
   ZBounds z;
-  z.lo = Scand + (uint64_t)fmax(slo, 0.0);
-  z.hi = (shi >= LIM) ? (1ull << 62) : Scand + (uint64_t)ceil(shi);
-  if (nz == 0) {
-    const uint64_t a = szl <= 0.0 ? 0ull : (uint64_t)szl;
-    const uint64_t c = szh >= LIM ? (1ull << 62) : (uint64_t)ceil(szh);
+  z.lo = Scand + (uint64_t)fmax(s.lo, 0.0);
+  z.hi = (s.hi >= LIM) ? (1ull << 62) : Scand + (uint64_t)ceil(s.hi);
+  if (s.nz == 0) {
+    const uint64_t a = s.zl <= 0.0 ? 0ull : (uint64_t)s.zl;
+    const uint64_t c = s.zh >= LIM ? (1ull << 62) : (uint64_t)ceil(s.zh);
     z.lo = a > z.lo ? a : z.lo;
     z.hi = c < z.hi ? c : z.hi;
   }
@@ -896,50 +913,27 @@ struct RegStore {
 // Register merge scratch.
 struct MergeSmem {
   uint64_t bucket[3][64];  // draw buckets, one array per radix level
+  // per lane, added by every listing wave: [0] hot mass, [1] hot mass at or
+  // above tcov, [2] cold mass; [3] level-0 draw buckets (4096 ids each) over
+  // every hot candidate
+  uint64_t acc[4][64];
+  ZParts zp;  // the summaries' share of the normaliser bounds
+  int n;      // hot candidates listed
 };
 
-// Normaliser bounds for the block merge: the same computation as z_bounds,
-// every thread reading the G summaries itself.
+// Normaliser bounds for the block merge: every thread reads the G summaries
+// itself.
 __device__ __forceinline__ ZBounds z_bounds_loop(const SliceHdr* hd, int G, float m, uint64_t Scand) {
-  const double SC = 17592186044416.0, EPS = 2e-4;
-  double slo = 0.0, shi = 0.0, szl = 0.0, szh = 0.0;
-  int nz = 0;
+  ZParts s{0.0, 0.0, 0.0, 0.0, 0};
   for (int l = 0; l < G; ++l) {
-    const SliceHdr& h = hd[l];
-    double lo = 0.0, hi = 0.0, zl = 0.0, zh = 0.0;
-    int no_zf = 0;
-    if (h.m != -INFINITY) {
-      auto wlo = [&](float t) {
-        return t == -INFINITY ? 0.0 : fmax(floor((double)expf(t - m) * SC * (1.0 - EPS)) - 1.0, 0.0);
-      };
-      lo = (double)h.g1 * wlo(h.t1) + (double)h.g2 * wlo(h.t2);
-      hi = (double)(h.nall - h.n) * ((double)expf(h.tau - m) * SC * (1.0 + EPS) + 1.0);
-      if (h.zf >= 0.0) {
-        const double sc = (double)expf(h.m - m) * SC;
-        zl = h.zf * sc * (1.0 - EPS) - (double)h.nall;
-        zh = h.zf * sc * (1.0 + EPS) + (double)h.nall;
-      } else {
-        no_zf = 1;
-      }
-    }
-    slo += lo;
-    shi += hi;
-    szl += zl;
-    szh += zh;
-    nz += no_zf;
+    const ZParts q = z_slice(hd[l], m);
+    s.lo += q.lo;
+    s.hi += q.hi;
+    s.zl += q.zl;
+    s.zh += q.zh;
+    s.nz += q.nz;
   }
-  const double LIM = 4.0e18;
-  ZBounds z;
-  z.lo = Scand + (uint64_t)fmax(slo, 0.0);
-  z.hi = (shi >= LIM) ? (1ull << 62) : Scand + (uint64_t)ceil(shi);
-  if (nz == 0) {
-    const uint64_t a = szl <= 0.0 ? 0ull : (uint64_t)szl;
-    const uint64_t c = szh >= LIM ? (1ull << 62) : (uint64_t)ceil(szh);
-    z.lo = a > z.lo ? a : z.lo;
-    z.hi = c < z.hi ? c : z.hi;
-  }
-  if (z.hi > (1ull << 62)) z.hi = 1ull << 62;
-  return z;
+  return z_finish(s, Scand);
 }
 
 // Candidates in LDS (any number), filtered by the whole workgroup: counts and
@@ -1042,91 +1036,147 @@ __device__ __forceinline__ bool run_filters(St& st, const SampleKArgs& a, const 
   return true;
 }
 
-// Register merge of row b by wave 0.  The row's N filterable candidates sit
-// densely in LDS (`cc`); slot t of lane l holds candidate 64 t + l, so NS is
-// ceil(N / 64) rounded up to a compiled slot count.  `zc` is this lane's
-// share of the exact mass of the candidates left out of the store (those
-// below the min-p threshold, which no chain can keep); it counts towards the
-// normaliser only.  Returns the path code (0 done, 3 exact engine).
-template <int G, int NS>
-__device__ __forceinline__ int merge_regs(const SampleKArgs& a, const FastPlan& P, int b, const RowParams& rp,
-                                          const SliceHdr& hd, float m, float tcov, float ub, const int2* cc, int N,
-                                          uint64_t zc, MergeSmem& sm) {
+// LDS list of the hot candidates (those that can still be kept): entry i is
+// cand[i] = (logit bits, id), mass[i] = exp_fix44(logit - m) and, when T != 1,
+// dw[i] = the draw weight exp_fix44(scaled logit).
+struct HotList {
+  int2* cand;
+  uint64_t* mass;
+  uint64_t* dw;
+};
+__device__ __forceinline__ HotList hot_list(char* dyn) {
+  HotList h;
+  h.cand = (int2*)dyn;
+  h.mass = (uint64_t*)(dyn + (size_t)QSPEC * 64 * sizeof(int2));
+  h.dw = h.mass + QSPEC * 64;
+  return h;
+}
+constexpr int DRAW_MEMBERS = 16;  // draw: bucket members resolved directly, at most
+constexpr size_t HOT_LIST_BYTES = (size_t)QSPEC * 64 * (sizeof(int2) + 2 * sizeof(uint64_t));
+
+// Register merge of row b by wave 0.  The row's N hot candidates sit in the
+// LDS list in no particular order (every step below is order independent);
+// slot t of lane l holds entry 64 t + l, so NS is ceil(N / 64) rounded up to
+// a compiled slot count.  The listing waves' per-lane partial sums are in
+// sm.acc, the summaries' share of the normaliser bounds in sm.zp.  Returns
+// the path code (0 done, 3 exact engine).
+template <int NS>
+__device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const RowParams& rp, float m, float tcov, float ub,
+                                          const HotList& hl, int N, MergeSmem& sm) {
   const int lane = threadIdx.x & 63;
+  const bool tscale = rp.T != 1.0f;
   RegStore<NS> st;
+  uint64_t wd[NS];
   st.al = 0;
   st.bkt = sm.bucket[0];
 #pragma unroll
   for (int t = 0; t < NS; ++t) {
     const bool valid = t * 64 + lane < N;
-    const int2 c = cc[valid ? t * 64 + lane : 0];
+    const int i = valid ? t * 64 + lane : 0;
+    const int2 c = hl.cand[i];
+    const uint64_t w = hl.mass[i];
+    wd[t] = tscale ? hl.dw[i] : 0ull;
     st.cl[t] = valid ? __int_as_float(c.x) : -INFINITY;
     st.ci[t] = valid ? c.y : -1;
+    st.w[t] = valid ? w : 0ull;
     st.al |= valid ? (1u << t) : 0u;
   }
-  // invalid slots hold -inf: exp_fix44 gives 0
-#pragma unroll
-  for (int t = 0; t < NS; ++t) st.w[t] = exp_fix44(st.cl[t] - m);
-  uint64_t Scand;
-  {
-    uint64_t mv[3] = {0ull, 0ull, zc};
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-      mv[0] += st.w[t];
-      mv[1] += st.cl[t] >= tcov ? st.w[t] : 0ull;
-    }
-    wsum_u64_k<3>(mv);
-    st.m_all = mv[0];
-    st.m_cov = mv[1];
-    st.cached = true;
-    Scand = mv[0] + mv[2];
-  }
-  const ZBounds zb = z_bounds<G>(hd, lane < G, m, Scand);
+  // the exact masses and the level-0 draw buckets: one interleaved scan of
+  // the per-lane partials (lane 63 ends with the totals)
+  uint64_t acc[4] = {sm.acc[0][lane], sm.acc[1][lane], sm.acc[2][lane], sm.acc[3][lane]};
+  const uint64_t b0 = acc[3];
+  wscan_incl_u64_k<4>(acc);
+  st.m_all = lane_u64(acc[0], 63);
+  st.m_cov = lane_u64(acc[1], 63);
+  st.cached = true;
+  const ZBounds zb = z_finish(sm.zp, st.m_all + lane_u64(acc[2], 63));
+  const uint32_t al0 = st.al;
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
 
   // Draw: integer inverse CDF in vocabulary order over the kept slots.
   const float invT = (float)(1.0 / (double)rp.T);
   const float Tc = (float)fmax((double)rp.T, 1e-5);
-  if (rp.T != 1.0f) {
+  if (tscale) {
 #pragma unroll
-    for (int t = 0; t < NS; ++t)
-      st.w[t] = st.on(t) ? exp_fix44(chain_scale(a.chain, st.cl[t] - m, invT, Tc)) : 0ull;
+    for (int t = 0; t < NS; ++t) st.w[t] = st.on(t) ? wd[t] : 0ull;
   }
   // The draw is the smallest id whose inclusive kept weight, in vocabulary
-  // order, exceeds the target.  The candidates are in no order, so it is a
-  // radix descent over the 18-bit id, 6 bits per level: each level adds the
-  // kept weights of the ids under the current prefix into 64 LDS buckets,
-  // scans the buckets across the lanes, and takes the first bucket whose
-  // inclusive sum exceeds the remaining target.  Level 0 covers every kept
-  // candidate, so its scan total is the normaliser ZV.
-  uint64_t ZV = 0;
-  uint32_t prefix = 0;
-  uint64_t rem = 0;
-  const int levels = a.tokens ? 3 : 1;
-#pragma unroll
-  for (int lev = 0; lev < 3; ++lev) sm.bucket[lev][lane] = 0;
-  wave_sync();
-  for (int lev = 0; lev < levels; ++lev) {
-    const int s = 12 - 6 * lev;
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-      if (st.on(t) && ((uint32_t)st.ci[t] >> (s + 6)) == prefix)
-        atomicAdd((unsigned long long*)&sm.bucket[lev][((uint32_t)st.ci[t] >> s) & 63u], (unsigned long long)st.w[t]);
-    }
+  // order, exceeds the target.  The candidates are in no order.  Level 0
+  // sums the kept weights of each block of 4096 ids (bucket d at lane d),
+  // scans the lanes and takes the first bucket whose inclusive sum exceeds
+  // the target; its scan total is the normaliser ZV.  When the filters kept
+  // every listed candidate, the listing waves' buckets are that sum already.
+  // Inside the chosen bucket, a handful of members is resolved directly:
+  // each member's inclusive weight over the members at or below its id,
+  // then the smallest id above the remaining target.  More members go
+  // through two more 6-bit radix levels.
+  const bool all_kept = __ballot(st.al != al0) == 0ull;
+  uint64_t incl0 = acc[3], bv0 = b0;
+  if (!all_kept) {
+    sm.bucket[0][lane] = 0;
     wave_sync();
-    const uint64_t bv = sm.bucket[lev][lane];
-    const uint64_t incl = wscan_incl_u64(bv);
-    if (lev == 0) {
-      ZV = lane_u64(incl, 63);
-      if (!ZV) break;
-      rem = draw_target(ub, ZV);
-    }
-    // a bucket exists: rem is below the prefix's total
-    const int bsel = (int)__ffsll((long long)__ballot(incl > rem)) - 1;
-    rem -= lane_u64(incl, bsel) - lane_u64(bv, bsel);
-    prefix = (prefix << 6) | (uint32_t)bsel;
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+      if (st.on(t)) atomicAdd((unsigned long long*)&sm.bucket[0][(uint32_t)st.ci[t] >> 12], (unsigned long long)st.w[t]);
+    wave_sync();
+    bv0 = sm.bucket[0][lane];
+    incl0 = wscan_incl_u64(bv0);
   }
-  if (a.tokens && lane == 0) a.tokens[b] = ZV ? (int)prefix : 0;
+  const uint64_t ZV = lane_u64(incl0, 63);
+  int tok = 0;
+  if (a.tokens && ZV) {
+    uint64_t rem = draw_target(ub, ZV);
+    // a bucket exists: rem is below the total
+    const int p0 = (int)__ffsll((long long)__ballot(incl0 > rem)) - 1;
+    rem -= lane_u64(incl0, p0) - lane_u64(bv0, p0);
+    auto member = [&](int t) { return st.on(t) && ((uint32_t)st.ci[t] >> 12) == (uint32_t)p0; };
+    int nmem = 0;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) nmem += ballot_count(member(t));
+    if (nmem <= DRAW_MEMBERS) {
+      uint64_t cum[NS];
+#pragma unroll
+      for (int t = 0; t < NS; ++t) cum[t] = 0;
+#pragma unroll
+      for (int t = 0; t < NS; ++t) {
+        uint64_t bits = __ballot(member(t));
+        while (bits) {
+          const int k = (int)__builtin_ctzll(bits);
+          bits &= bits - 1;
+          const uint32_t idk = lane_u32((uint32_t)st.ci[t], k);
+          const uint64_t wk = lane_u64(st.w[t], k);
+#pragma unroll
+          for (int q = 0; q < NS; ++q) cum[q] += (uint32_t)st.ci[q] >= idk ? wk : 0ull;
+        }
+      }
+      uint32_t best = 0xFFFFFFFFu;
+#pragma unroll
+      for (int t = 0; t < NS; ++t)
+        if (member(t) && cum[t] > rem) best = min(best, (uint32_t)st.ci[t]);
+      tok = (int)wmin_u32(best);
+    } else {
+      uint32_t prefix = (uint32_t)p0;
+      sm.bucket[1][lane] = 0;
+      sm.bucket[2][lane] = 0;
+      wave_sync();
+      for (int lev = 1; lev < 3; ++lev) {
+        const int sh = 12 - 6 * lev;
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+          if (st.on(t) && ((uint32_t)st.ci[t] >> (sh + 6)) == prefix)
+            atomicAdd((unsigned long long*)&sm.bucket[lev][((uint32_t)st.ci[t] >> sh) & 63u], (unsigned long long)st.w[t]);
+        }
+        wave_sync();
+        const uint64_t bv = sm.bucket[lev][lane];
+        const uint64_t incl = wscan_incl_u64(bv);
+        const int bsel = (int)__ffsll((long long)__ballot(incl > rem)) - 1;
+        rem -= lane_u64(incl, bsel) - lane_u64(bv, bsel);
+        prefix = (prefix << 6) | (uint32_t)bsel;
+      }
+      tok = (int)prefix;
+    }
+  }
+  if (a.tokens && lane == 0) a.tokens[b] = tok;
   if (a.kept) {
     const int nkept = st.count();
     if (lane == 0) a.kept[b] = nkept;
@@ -1213,115 +1263,156 @@ __device__ __noinline__ int merge_block(const SampleKArgs* ap, const FastPlan* p
 }
 
 template <int G>
-__global__ void __launch_bounds__(512) merge_kernel(SampleKArgs a, FastPlan P) {
+__global__ void __launch_bounds__(MW * 64) merge_kernel(SampleKArgs a, FastPlan P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ ExactSmem esm;
   __shared__ MergeSmem sm;
   __shared__ int s_path;
-  __shared__ float s_m, s_tcov, s_ub;
   const int b = blockIdx.x;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const RowRaw raw = row_raw(a, b);
   const RowParams rp = row_params(a, raw, P.rule_cap);
-  if (tid < 64) {
-    const int lane = tid;
-    // one round trip: the summaries (lane s < G), the row's uniform and the
-    // first QSPEC candidate chunks (slot t: chunk t / G of slice t % G).
-    // Every load is unconditional from an in-bounds address (lanes >= G read
-    // a duplicate summary, chunks past a slice's count stale entries, both
-    // ignored), so no branch join waits for a load to land.
-    const SliceHdr hd = P.hdr[(long long)b * G + min(lane, G - 1)];
-    const float ub = (a.tokens && !rp.greedy) ? a.u[b] : 0.0f;
-    int2 spec[QSPEC];
+  // One round trip per wave: the summaries (lane s < G), the row's uniform
+  // and the wave's QW candidate chunks (slot t = QW wv + j: chunk t / G of
+  // slice t % G).  Every load is unconditional from an in-bounds address
+  // (lanes >= G read a duplicate summary, chunks past a slice's count stale
+  // entries, both ignored), so no branch join waits for a load to land.
+  const SliceHdr hd = P.hdr[(long long)b * G + min(lane, G - 1)];
+  const float ub = (a.tokens && !rp.greedy) ? a.u[b] : 0.0f;
+  int2 spec[QW];
 #pragma unroll
-    for (int t = 0; t < QSPEC; ++t) spec[t] = P.cand[((long long)b * G + t % G) * P.cap + (t / G) * 64 + lane];
-    // compiler barrier: keep every load above issued here, before anything
-    // waits on the summaries (no hardware wait is implied)
-    asm volatile("" ::: "memory");
-    // the G summaries sit in lanes 0..G-1: aggregate them with readlanes
-    float m = -INFINITY, tcov = -INFINITY;
-    int fl = 0, nmax = 0;
-#pragma unroll
-    for (int l = 0; l < G; ++l) {
-      m = fmaxf(m, __uint_as_float(lane_u32(__float_as_uint(hd.m), l)));
-      tcov = fmaxf(tcov, __uint_as_float(lane_u32(__float_as_uint(hd.tau), l)));
-      fl |= (int)lane_u32((uint32_t)hd.flags, l);
-      nmax = max(nmax, (int)lane_u32((uint32_t)hd.n, l));
-    }
-    const int flagged = fl & HDR_OVERFLOW;
-    int path;
-    if (rp.greedy) {
-      const int bi = wmin_i((lane < G && hd.m == m) ? hd.best_i : 0x7FFFFFFF);
-      if (flagged) {
-        path = 1;
-      } else {
-        if (lane == 0) {
-          if (a.tokens) a.tokens[b] = bi == 0x7FFFFFFF ? 0 : bi;
-          if (a.kept) a.kept[b] = 1;
-        }
-        path = 2;
-      }
-    } else if (flagged || rp.all) {
-      path = 1;
-    } else {
-      const int TS = (nmax + 63) / 64;
-      if (G * TS <= QSPEC) {
-        // Compact the loaded chunks into LDS.  Chunk t holds lanes
-        // [0, cnt_t) (a slice's candidates are a prefix of its list).  When
-        // min-p is the chain's last filter on the candidates (every chain but
-        // mlx_lm's top-k + top-p), a candidate below thr = m + ln min_p can
-        // never be kept: only its exact mass matters (to the normaliser), so
-        // it is summed here and left out.  Elsewhere thr is -inf and every
-        // candidate is filtered.
-        int2* cc = (int2*)dyn;
-        const bool split = rp.use_m && !(a.chain == WH_CHAIN_MLX && rp.use_k && rp.use_p);
-        const float thr = split ? m + min_p_log(a, rp.min_p) : -INFINITY;
-        const int hn = lane < G ? hd.n : 0;
-        int nsl[G];
-#pragma unroll
-        for (int l = 0; l < G; ++l) nsl[l] = (int)lane_u32((uint32_t)hn, l);
-        int N = 0;
-        uint64_t zc = 0;
-#pragma unroll
-        for (int t = 0; t < QSPEC; ++t) {
-          // cnt is wave uniform: empty chunks are skipped by a scalar branch
-          const int cnt = min(max(nsl[t % G] - (t / G) * 64, 0), 64);
-          if (cnt > 0) {
-            const float l = __int_as_float(spec[t].x);
-            const bool v = lane < cnt;
-            const bool hot = v && l >= thr;
-            if (split) zc += (v && !hot) ? exp_fix44(l - m) : 0ull;
-            const uint64_t bh = __ballot(hot);
-            if (hot) cc[N + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bh >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bh, 0u))] = spec[t];
-            N += (int)__popcll(bh);
-          }
-        }
-        wave_sync();
-        if (N <= 64) path = merge_regs<G, 1>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
-        else if (N <= 128) path = merge_regs<G, 2>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
-        else if (N <= 256) path = merge_regs<G, 4>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
-        else if (N <= 512) path = merge_regs<G, 8>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
-        else path = merge_regs<G, QM>(a, P, b, rp, hd, m, tcov, ub, cc, N, zc, sm);
-      } else {
-        path = 5;  // too many for registers: the whole workgroup merges
-        if (lane == 0) {
-          s_m = m;
-          s_tcov = tcov;
-          s_ub = ub;
-        }
-      }
-    }
-    if (lane == 0) {
-      s_path = path;
-      if (path != 5) P.path[b] = path;
-    }
+  for (int j = 0; j < QW; ++j) {
+    const int t = wv * QW + j;
+    spec[j] = P.cand[((long long)b * G + t % G) * P.cap + (t / G) * 64 + lane];
   }
+  // the list counter and the per-lane sums are zero before any wave adds to
+  // them (the barrier waits for none of the loads above)
+  if (tid == 0) sm.n = 0;
+  if (tid < 4 * 64) (&sm.acc[0][0])[tid] = 0ull;
   __syncthreads();
-  int path = s_path;
-  if (path == 5) {
-    path = merge_block(&kernargs()->a, &kernargs()->p, b, rp, G, s_m, s_tcov, s_ub, dyn, &esm);
+  // the G summaries sit in lanes 0..G-1: aggregate them with readlanes
+  float m = -INFINITY, tcov = -INFINITY;
+  int fl = 0, nmax = 0;
+#pragma unroll
+  for (int l = 0; l < G; ++l) {
+    m = fmaxf(m, __uint_as_float(lane_u32(__float_as_uint(hd.m), l)));
+    tcov = fmaxf(tcov, __uint_as_float(lane_u32(__float_as_uint(hd.tau), l)));
+    fl |= (int)lane_u32((uint32_t)hd.flags, l);
+    nmax = max(nmax, (int)lane_u32((uint32_t)hd.n, l));
+  }
+  const int flagged = fl & HDR_OVERFLOW;
+  // the path is the same in every wave: 0 register merge, 1 exact engine,
+  // 2 greedy, 5 block merge (too many candidates for the loaded chunks)
+  int path;
+  if (rp.greedy) path = flagged ? 1 : 2;
+  else if (flagged || rp.all) path = 1;
+  else path = G * ((nmax + 63) / 64) <= QSPEC ? 0 : 5;
+  if (path == 2) {
+    if (wv == 0) {
+      const int bi = wmin_i((lane < G && hd.m == m) ? hd.best_i : 0x7FFFFFFF);
+      if (lane == 0) {
+        if (a.tokens) a.tokens[b] = bi == 0x7FFFFFFF ? 0 : bi;
+        if (a.kept) a.kept[b] = 1;
+        P.path[b] = 2;
+      }
+    }
+    return;
+  }
+  if (path == 0) {
+    // Every wave lists the candidates of its chunks.  Chunk t holds lanes
+    // [0, cnt_t) (a slice's candidates are a prefix of its list).  When
+    // min-p is the chain's last filter on the candidates (every chain but
+    // mlx_lm's top-k + top-p), a candidate below thr = m + ln min_p can never
+    // be kept: only its exact mass matters (to the normaliser), so it is
+    // summed and left out of the list.  Elsewhere thr is -inf and every
+    // candidate is listed.  Each lane adds its three masses to its own LDS
+    // sums, and every listed candidate its draw weight to the level-0 draw
+    // bucket of its id; wave 0 scans both.
+    const HotList hl = hot_list(dyn);
+    const bool split = rp.use_m && !(a.chain == WH_CHAIN_MLX && rp.use_k && rp.use_p);
+    const float thr = split ? m + min_p_log(a, rp.min_p) : -INFINITY;
+    const bool tscale = rp.T != 1.0f;
+    const float invT = (float)(1.0 / (double)rp.T);
+    const float Tc = (float)fmax((double)rp.T, 1e-5);
+    const int hn = lane < G ? hd.n : 0;
+    uint64_t mv[3] = {0ull, 0ull, 0ull};  // hot mass, covered hot mass, cold mass
+    uint64_t e[QW], bh[QW];
+    int H = 0;
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < QW; ++j) {
+      const int t = wv * QW + j;
+      // cnt is wave uniform: an empty chunk is skipped by a scalar branch
+      const int cnt = min(max((int)lane_u32((uint32_t)hn, t % G) - (t / G) * 64, 0), 64);
+      e[j] = 0ull;
+      bh[j] = 0ull;
+      if (cnt > 0) {
+        any = true;
+        const float l = __int_as_float(spec[j].x);
+        const bool v = lane < cnt;
+        const bool hot = v && l >= thr;
+        const uint64_t ej = exp_fix44(l - m);
+        mv[0] += hot ? ej : 0ull;
+        mv[1] += (hot && l >= tcov) ? ej : 0ull;
+        mv[2] += (v && !hot) ? ej : 0ull;
+        e[j] = ej;
+        bh[j] = __ballot(hot);
+        H += (int)__popcll(bh[j]);
+      }
+    }
+    int base = 0;
+    if (H > 0) {
+      int r = 0;
+      if (lane == 0) r = atomicAdd(&sm.n, H);
+      base = __builtin_amdgcn_readfirstlane(r);
+    }
+#pragma unroll
+    for (int j = 0; j < QW; ++j) {
+      if ((bh[j] >> lane) & 1ull) {
+        const int i = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bh[j] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bh[j], 0u));
+        uint64_t dw = e[j];
+        if (tscale) {
+          dw = exp_fix44(chain_scale(a.chain, __int_as_float(spec[j].x) - m, invT, Tc));
+          hl.dw[i] = dw;
+        }
+        hl.cand[i] = spec[j];
+        hl.mass[i] = e[j];
+        atomicAdd((unsigned long long*)&sm.acc[3][(uint32_t)spec[j].y >> 12], (unsigned long long)dw);
+      }
+      base += (int)__popcll(bh[j]);
+    }
+    if (any) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) atomicAdd((unsigned long long*)&sm.acc[k][lane], (unsigned long long)mv[k]);
+    }
+    // the summaries' share of the normaliser bounds, beside the list (the
+    // last wave's chunks are the ones most often empty)
+    if (wv == MW - 1) {
+      const ZParts zp = z_parts<G>(hd, lane < G, m);
+      if (lane == 0) sm.zp = zp;
+    }
+    __syncthreads();
+    if (wv == 0) {
+      const int N = sm.n;
+      if (N <= 64) path = merge_regs<1>(a, b, rp, m, tcov, ub, hl, N, sm);
+      else if (N <= 128) path = merge_regs<2>(a, b, rp, m, tcov, ub, hl, N, sm);
+      else if (N <= 256) path = merge_regs<4>(a, b, rp, m, tcov, ub, hl, N, sm);
+      else if (N <= 512) path = merge_regs<8>(a, b, rp, m, tcov, ub, hl, N, sm);
+      else path = merge_regs<QM>(a, b, rp, m, tcov, ub, hl, N, sm);
+      if (lane == 0) {
+        s_path = path;
+        P.path[b] = path;
+      }
+    }
+    __syncthreads();
+    path = s_path;
+  } else if (path == 5) {
+    path = merge_block(&kernargs()->a, &kernargs()->p, b, rp, G, m, tcov, ub, dyn, &esm);
     if (tid == 0) P.path[b] = path;
     __syncthreads();
+  } else if (tid == 0) {
+    P.path[b] = path;
   }
   if (path == 1 || path == 3) exact_row(kernargs()->a, b, dyn, esm);
 }
@@ -1430,7 +1521,7 @@ static int launch_merge_t(const SampleKArgs& k, const FastPlan& fp, size_t lds, 
   auto fn = merge_kernel<G>;
   int rc = set_lds((const void*)fn, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(fn, dim3(k.B), dim3(512), lds, st, k, fp);
+  hipLaunchKernelGGL(fn, dim3(k.B), dim3(MW * 64), lds, st, k, fp);
   return WH_OK;
 }
 
@@ -1466,7 +1557,7 @@ int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st
   fp.path = (int*)(ws + wl.path);
   fp.hdr = (SliceHdr*)(ws + wl.hdr);
   fp.cand = (int2*)(ws + wl.cand);
-  const size_t lds_merge = std::max((size_t)hp.G * hp.cap * 8, penalty_lds_bytes(k));
+  const size_t lds_merge = std::max({(size_t)hp.G * hp.cap * 8, penalty_lds_bytes(k), HOT_LIST_BYTES});
   int rc = launch_slice(k.dtype, hp.R, k, fp, hp.lds, st);
   if (rc) return rc;
   hipError_t e = hipGetLastError();
