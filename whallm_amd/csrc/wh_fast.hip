@@ -106,16 +106,34 @@ struct RowParams {
   bool all;  // nothing bounds the kept set: exact engine
 };
 
-// Both kernels take (SampleKArgs, FastPlan); their kernel-argument segment
-// holds SampleKArgs at offset 0 and FastPlan at the next 8-byte boundary.
-// Reading fields in place (a pointer, not a copy) keeps out-of-line callees
-// and per-row parameter loads from forcing the arguments into private memory.
-struct KernArgs {
+// Both kernels take first the scalars and pointers their first loads need
+// (leading scalar arguments are preloaded into SGPRs at wave launch, so
+// those loads wait for no argument fetch), then (SampleKArgs, FastPlan).
+// The structures mirror the argument segments.  Reading fields in place (a
+// pointer, not a copy) keeps out-of-line callees and per-row parameter loads
+// from forcing the arguments into private memory.
+struct SliceKernArgs {
+  const char* logits;
+  const int32_t* hist;
+  long long row_stride;  // elements
+  int G, SL, V, hs;      // hs: history row stride
+  int pen;               // penalties on
   SampleKArgs a;
   FastPlan p;
 };
-__device__ __forceinline__ const KernArgs* kernargs() {
-  return (const KernArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+struct MergeKernArgs {
+  const SliceHdr* hdr;
+  const int2* cand;
+  SampleKArgs a;
+  FastPlan p;
+};
+static_assert(offsetof(SliceKernArgs, a) == 48, "slice kernel argument layout");
+static_assert(offsetof(MergeKernArgs, a) == 16, "merge kernel argument layout");
+__device__ __forceinline__ const SliceKernArgs* slice_kernargs() {
+  return (const SliceKernArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+}
+__device__ __forceinline__ const MergeKernArgs* merge_kernargs() {
+  return (const MergeKernArgs*)__builtin_amdgcn_kernarg_segment_ptr();
 }
 
 // Which bounds the slices may use.  Chain MLX with top-k and top-p computes
@@ -132,8 +150,8 @@ struct RowRaw {
 // scalar loads, counted apart from the vector loads of the logits.
 typedef __attribute__((address_space(4))) const float cfloat;
 typedef __attribute__((address_space(4))) const int cint;
-__device__ __forceinline__ RowRaw row_raw(const SampleKArgs& a, int b) {
-  const SampleKArgs& ka = kernargs()->a;
+// ka is the kernel's own argument copy (in its argument segment).
+__device__ __forceinline__ RowRaw row_raw(const SampleKArgs& a, const SampleKArgs& ka, int b) {
   RowRaw r;
   r.T = *(cfloat*)(a.T_rows ? a.T_rows + b : &ka.T);
   r.top_p = *(cfloat*)(a.top_p_rows ? a.top_p_rows + b : &ka.top_p);
@@ -361,27 +379,26 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
 }
 
 template <int DT, int R>
-__global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
+__global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logits, const int32_t* __restrict__ hist,
+                                                   long long row_stride, int G, int SL, int V, int hs, int pen,
+                                                   SampleKArgs a, FastPlan P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ SliceSmem sm;
   constexpr int EPT = DT ? 8 : 4;
   constexpr int ESZ = DT ? 2 : 4;
   constexpr uint32_t NEG = DT ? 0xFF80FF80u : 0xFF800000u;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int b = blockIdx.x / P.G, s = blockIdx.x - b * P.G;
-  const int V = a.V;
-  const int v0 = s * P.SL, v1 = min(V, v0 + P.SL);
+  const int b = blockIdx.x / G, s = blockIdx.x - b * G;
+  const int v0 = s * SL, v1 = min(V, v0 + SL);
 
-  // 1. loads, in the order they are needed: the row's parameters (scalar),
-  //    the history window (up to 4 ids per thread) and its length, then the
-  //    slice straight into registers (padding groups read as -inf).  Vector
+  // 1. loads, in the order they are needed: the history window (up to 4 ids
+  //    per thread) and its length, then the slice straight into registers
+  //    (padding groups read as -inf), then the row's parameters (scalar).
+  //    Their addresses come from the preloaded leading arguments.  Vector
   //    loads complete in order, so waiting for the history leaves the logits
   //    in flight; the compiler barrier keeps every load issued before the
   //    first wait.
-  const RowRaw raw = row_raw(a, b);
-  const bool pen = a.hcap > 0;
   constexpr int HPF = WH_MAX_WINDOW / FT;  // history positions per thread
-  const int hs = (int)a.hist_stride;
   const bool pf = hs <= HPF * FT;  // the whole history row fits the prefetch
   int hreg[HPF];
   int len = 0, jbase = 0;
@@ -390,7 +407,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   // Every vector load is unconditional, from a clamped in-bounds address, so
   // the number of loads in flight is the same on every path and each wait is
   // for exactly the loads it needs.
-  const int32_t* hrow = a.hist + (long long)b * a.hist_stride;
+  const int32_t* hrow = hist + (long long)b * hs;
   if (pen) {
     if (pf) {
       // the addresses do not need the length, which is read after the
@@ -407,7 +424,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
       for (int q = 0; q < HPF; ++q) hreg[q] = hrow[min(jbase + tid + q * FT, hs - 1)];
     }
   }
-  const char* rowp = (const char*)a.logits + (size_t)b * a.row_stride * ESZ;
+  const char* rowp = logits + (size_t)b * row_stride * ESZ;
   uint4 d[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -416,8 +433,9 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   }
   asm volatile("" ::: "memory");
   if (pen && pf) len = max(0, min(*(cint*)(a.hist_len + b), hs));
+  const RowRaw raw = row_raw(a, slice_kernargs()->a, b);
   const RowParams rp = row_params(a, raw, P.rule_cap);
-  SliceHdr* hdr = P.hdr + (long long)b * P.G + s;
+  SliceHdr* hdr = P.hdr + (long long)b * G + s;
   if (rp.all) {
     if (tid == 0) hdr->flags = HDR_OVERFLOW;
     return;
@@ -435,20 +453,19 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   //    the repetition / presence flags.  The in-window history ids of this
   //    slice enter it with LDS atomics; the thread whose atomic first touches
   //    an element owns it.  All of this needs only the history, so it runs
-  //    while the logits are still in flight.  Owners then keep the final code
-  //    and mark the element with all-ones.  As each 16-byte group lands, its
-  //    holder ANDs the codes into a copy (the raw bits of marked elements),
-  //    writes that back into the code slots, and ORs the codes into the
-  //    registers: a penalised element becomes a NaN there, which every max
-  //    and >= test ignores.  After one more barrier the owners read the raw
-  //    bits, apply the penalties and list the element, which lives on only in
-  //    the list.
+  //    while the logits are still in flight.  Owners then keep the final code,
+  //    mark the element with all-ones and fetch its logit from memory (a
+  //    2- or 4-byte gather that overlaps the groups landing).  As each 16-byte
+  //    group lands, its holder ORs the codes into the registers: a penalised
+  //    element becomes a NaN there, which every max and >= test ignores.  The
+  //    owners apply the penalties to the fetched values and list the
+  //    elements, which live on only in the list.
   char* codes = dyn;
   int2* patch = (int2*)(dyn + P.codes_bytes);
   float pmax = -INFINITY;
   PenCtx pc;
   uint32_t own = 0;
-  uint32_t ocode[HPF];
+  uint32_t ocode[HPF], oraw[HPF];
   if (pen) {
     pc.rep = a.rep;
     pc.pres = a.pres;
@@ -492,6 +509,20 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
       }
       if (((old >> sh) & 0xFFFFu) == 0u) own |= 1u << q;
     }
+  }
+  // The owners' gathers, issued as soon as ownership is known so that their
+  // latency overlaps the two barriers and the group loop below.  They are
+  // issued on every path (other lanes, and every lane without penalties,
+  // read the slice's first element: one shared line), so the waits for the
+  // groups count the same loads on every path and never wait for a gather;
+  // the values are first used at the apply.  A bfloat16 owner reads the
+  // aligned word holding its element (V is even on this path).
+#pragma unroll
+  for (int q = 0; q < HPF; ++q) {
+    const int t = ((own >> q) & 1u) ? hreg[q] : v0;
+    oraw[q] = ((const uint32_t*)rowp)[DT ? (t >> 1) : t];
+  }
+  if (pen) {
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < HPF; ++q) {
@@ -516,10 +547,8 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
   for (int r = 0; r < R; ++r) {
     const int g = v0 + (r * FT + tid) * EPT;
     if (pen && g < v1) {
-      uint4* cp = (uint4*)(codes + (size_t)(g - v0) * ESZ);
-      const uint4 cw = *cp;
+      const uint4 cw = *(const uint4*)(codes + (size_t)(g - v0) * ESZ);
       if ((cw.x | cw.y | cw.z | cw.w) != 0u) {
-        *cp = make_uint4(d[r].x & cw.x, d[r].y & cw.y, d[r].z & cw.z, d[r].w & cw.w);
         d[r].x |= cw.x;
         d[r].y |= cw.y;
         d[r].z |= cw.z;
@@ -531,14 +560,16 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
     mx = fmaxf(mx, gm[r]);
   }
   if (pen) {
-    __syncthreads();
 #pragma unroll
     for (int q = 0; q < HPF; ++q) {
       if (!((own >> q) & 1u)) continue;
       const int t = hreg[q];
-      const float l = (DT ? __uint_as_float((uint32_t)((uint16_t*)codes)[t - v0] << 16)
-                          : __uint_as_float(((uint32_t*)codes)[t - v0])) + 0.0f;
-      const float v = pc.apply(l, ocode[q]);
+      // the empty asm redefines the gathered bits here, so their first use
+      // (and the wait for them) cannot be hoisted above the group loop
+      uint32_t raw = oraw[q];
+      asm volatile("" : "+v"(raw));
+      if (DT) raw = (t & 1) ? (raw & 0xFFFF0000u) : (raw << 16);
+      const float v = pc.apply(__uint_as_float(raw) + 0.0f, ocode[q]);
       const int slot = atomicAdd(&sm.npatch, 1);
       if (slot < P.pcap) patch[slot] = make_int2(__float_as_int(v), t);
       pmax = fmaxf(pmax, v);
@@ -606,7 +637,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(SampleKArgs a, FastPlan P) {
 
   // 5. candidates from the groups whose max reaches tau, written straight to
   //    the workspace; group band counts; optional hardware-exp sum
-  int2* gc = P.cand + ((long long)b * P.G + s) * P.cap;
+  int2* gc = P.cand + ((long long)b * G + s) * P.cap;
   // groups (and listed penalised elements) at or above tau, t1 and t2; the
   // band counts are the differences (a NaN group max counts nowhere)
   int c0 = 0, c1 = 0, c2 = 0;
@@ -1263,7 +1294,8 @@ __device__ __noinline__ int merge_block(const SampleKArgs* ap, const FastPlan* p
 }
 
 template <int G>
-__global__ void __launch_bounds__(MW * 64) merge_kernel(SampleKArgs a, FastPlan P) {
+__global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restrict__ hdr, const int2* __restrict__ cand,
+                                                         SampleKArgs a, FastPlan P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ ExactSmem esm;
   __shared__ MergeSmem sm;
@@ -1271,21 +1303,23 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(SampleKArgs a, FastPlan 
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const RowRaw raw = row_raw(a, b);
-  const RowParams rp = row_params(a, raw, P.rule_cap);
-  // One round trip per wave: the summaries (lane s < G), the row's uniform
-  // and the wave's QW candidate chunks (slot t = QW wv + j: chunk t / G of
-  // slice t % G).  Every load is unconditional from an in-bounds address
-  // (lanes >= G read a duplicate summary, chunks past a slice's count stale
-  // entries, both ignored), so no branch join waits for a load to land.
-  const SliceHdr hd = P.hdr[(long long)b * G + min(lane, G - 1)];
-  const float ub = (a.tokens && !rp.greedy) ? a.u[b] : 0.0f;
+  // One round trip per wave, issued first (its pointers are preloaded
+  // arguments): the summaries (lane s < G) and the wave's QW candidate
+  // chunks (slot t = QW wv + j: chunk t / G of slice t % G).  Every load is
+  // unconditional from an in-bounds address (lanes >= G read a duplicate
+  // summary, chunks past a slice's count stale entries, both ignored), so no
+  // branch join waits for a load to land.
+  const SliceHdr hd = hdr[(long long)b * G + min(lane, G - 1)];
   int2 spec[QW];
 #pragma unroll
   for (int j = 0; j < QW; ++j) {
     const int t = wv * QW + j;
-    spec[j] = P.cand[((long long)b * G + t % G) * P.cap + (t / G) * 64 + lane];
+    spec[j] = cand[((long long)b * G + t % G) * FAST_CAP + (t / G) * 64 + lane];
   }
+  asm volatile("" ::: "memory");
+  const RowRaw raw = row_raw(a, merge_kernargs()->a, b);
+  const RowParams rp = row_params(a, raw, P.rule_cap);
+  const float ub = (a.tokens && !rp.greedy) ? a.u[b] : 0.0f;
   // the list counter and the per-lane sums are zero before any wave adds to
   // them (the barrier waits for none of the loads above)
   if (tid == 0) sm.n = 0;
@@ -1408,13 +1442,13 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(SampleKArgs a, FastPlan 
     __syncthreads();
     path = s_path;
   } else if (path == 5) {
-    path = merge_block(&kernargs()->a, &kernargs()->p, b, rp, G, m, tcov, ub, dyn, &esm);
+    path = merge_block(&merge_kernargs()->a, &merge_kernargs()->p, b, rp, G, m, tcov, ub, dyn, &esm);
     if (tid == 0) P.path[b] = path;
     __syncthreads();
   } else if (tid == 0) {
     P.path[b] = path;
   }
-  if (path == 1 || path == 3) exact_row(kernargs()->a, b, dyn, esm);
+  if (path == 1 || path == 3) exact_row(merge_kernargs()->a, b, dyn, esm);
 }
 
 // ---------------------------------------------------------------------------
@@ -1490,7 +1524,8 @@ static int launch_slice_t(const SampleKArgs& k, const FastPlan& fp, size_t lds, 
   auto fn = slice_kernel<DT, R>;
   int rc = set_lds((const void*)fn, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(fn, dim3(k.B * fp.G), dim3(FT), lds, st, k, fp);
+  hipLaunchKernelGGL(fn, dim3(k.B * fp.G), dim3(FT), lds, st, (const char*)k.logits, k.hist, (long long)k.row_stride, fp.G,
+                     fp.SL, k.V, (int)k.hist_stride, k.hcap > 0 ? 1 : 0, k, fp);
   return WH_OK;
 }
 
@@ -1521,7 +1556,7 @@ static int launch_merge_t(const SampleKArgs& k, const FastPlan& fp, size_t lds, 
   auto fn = merge_kernel<G>;
   int rc = set_lds((const void*)fn, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(fn, dim3(k.B), dim3(MW * 64), lds, st, k, fp);
+  hipLaunchKernelGGL(fn, dim3(k.B), dim3(MW * 64), lds, st, (const SliceHdr*)fp.hdr, (const int2*)fp.cand, k, fp);
   return WH_OK;
 }
 
