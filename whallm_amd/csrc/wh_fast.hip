@@ -950,6 +950,7 @@ struct MergeSmem {
   uint64_t acc[4][64];
   ZParts zp;  // the summaries' share of the normaliser bounds
   int n;      // hot candidates listed
+  int tok;    // wave 1's draw over the whole list
 };
 
 // Normaliser bounds for the block merge: every thread reads the G summaries
@@ -1085,12 +1086,117 @@ __device__ __forceinline__ HotList hot_list(char* dyn) {
 constexpr int DRAW_MEMBERS = 16;  // draw: bucket members resolved directly, at most
 constexpr size_t HOT_LIST_BYTES = (size_t)QSPEC * 64 * (sizeof(int2) + 2 * sizeof(uint64_t));
 
+// The draw is the smallest id whose inclusive kept weight, in vocabulary
+// order, exceeds the target draw_target(u, ZV).  The candidates are in no
+// order.  Level 0 sums the kept weights of each block of 4096 ids (bucket d
+// at lane d), scans the lanes and takes the first bucket whose inclusive sum
+// exceeds the target; its scan total is the normaliser ZV.  Inside the
+// chosen block, a handful of members is resolved directly: each member's
+// inclusive weight over the members at or below its id, then the smallest
+// id above the remaining target.  More members go through two more 6-bit
+// radix levels (LDS buckets 1 and 2).
+//
+// Level 0: the chosen block, and rem reduced to the remainder inside it
+// (incl0 / bv0: the lane's inclusive scan and bucket; ZV > 0).
+__device__ __forceinline__ int draw_level0(uint64_t incl0, uint64_t bv0, uint64_t ZV, float u, uint64_t& rem) {
+  rem = draw_target(u, ZV);
+  // a bucket exists: rem is below the total
+  const int p0 = (int)__ffsll((long long)__ballot(incl0 > rem)) - 1;
+  rem -= lane_u64(incl0, p0) - lane_u64(bv0, p0);
+  return p0;
+}
+// Inside block p0, over the slots in `on` (ids ci, weights w).
+template <int NS>
+__device__ __forceinline__ int draw_in_block(const int (&ci)[NS], const uint64_t (&w)[NS], uint32_t on, int p0, uint64_t rem,
+                                             MergeSmem& sm) {
+  const int lane = threadIdx.x & 63;
+  auto member = [&](int t) { return ((on >> t) & 1u) && ((uint32_t)ci[t] >> 12) == (uint32_t)p0; };
+  int nmem = 0;
+#pragma unroll
+  for (int t = 0; t < NS; ++t) nmem += ballot_count(member(t));
+  if (nmem <= DRAW_MEMBERS) {
+    uint64_t cum[NS];
+#pragma unroll
+    for (int t = 0; t < NS; ++t) cum[t] = 0;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      uint64_t bits = __ballot(member(t));
+      while (bits) {
+        const int k = (int)__builtin_ctzll(bits);
+        bits &= bits - 1;
+        const uint32_t idk = lane_u32((uint32_t)ci[t], k);
+        const uint64_t wk = lane_u64(w[t], k);
+#pragma unroll
+        for (int q = 0; q < NS; ++q) cum[q] += (uint32_t)ci[q] >= idk ? wk : 0ull;
+      }
+    }
+    uint32_t best = 0xFFFFFFFFu;
+#pragma unroll
+    for (int t = 0; t < NS; ++t)
+      if (member(t) && cum[t] > rem) best = min(best, (uint32_t)ci[t]);
+    return (int)wmin_u32(best);
+  }
+  uint32_t prefix = (uint32_t)p0;
+  sm.bucket[1][lane] = 0;
+  sm.bucket[2][lane] = 0;
+  wave_sync();
+  for (int lev = 1; lev < 3; ++lev) {
+    const int sh = 12 - 6 * lev;
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      if (((on >> t) & 1u) && ((uint32_t)ci[t] >> (sh + 6)) == prefix)
+        atomicAdd((unsigned long long*)&sm.bucket[lev][((uint32_t)ci[t] >> sh) & 63u], (unsigned long long)w[t]);
+    }
+    wave_sync();
+    const uint64_t bv = sm.bucket[lev][lane];
+    const uint64_t incl = wscan_incl_u64(bv);
+    const int bsel = (int)__ffsll((long long)__ballot(incl > rem)) - 1;
+    rem -= lane_u64(incl, bsel) - lane_u64(bv, bsel);
+    prefix = (prefix << 6) | (uint32_t)bsel;
+  }
+  return (int)prefix;
+}
+
+// The draw of row b over every listed hot candidate, by wave 1 while wave 0
+// runs the filters: it is the row's draw whenever the filters keep the whole
+// list (level 0 is then the listing waves' buckets).  Lane 0 leaves the
+// token in sm.tok.
+template <int NS>
+__device__ __forceinline__ void spec_draw(bool tscale, float ub, const HotList& hl, int N, MergeSmem& sm) {
+  const int lane = threadIdx.x & 63;
+  int ci[NS];
+  uint64_t w[NS];
+  uint32_t on = 0;
+#pragma unroll
+  for (int t = 0; t < NS; ++t) {
+    const bool valid = t * 64 + lane < N;
+    const int i = valid ? t * 64 + lane : 0;
+    const int id = hl.cand[i].y;
+    const uint64_t x = tscale ? hl.dw[i] : hl.mass[i];
+    ci[t] = valid ? id : -1;
+    w[t] = valid ? x : 0ull;
+    on |= valid ? (1u << t) : 0u;
+  }
+  const uint64_t bv0 = sm.acc[3][lane];
+  const uint64_t incl0 = wscan_incl_u64(bv0);
+  const uint64_t ZV = lane_u64(incl0, 63);
+  int tok = 0;
+  if (ZV) {
+    uint64_t rem;
+    const int p0 = draw_level0(incl0, bv0, ZV, ub, rem);
+    tok = draw_in_block<NS>(ci, w, on, p0, rem, sm);
+  }
+  if (lane == 0) sm.tok = tok;
+}
+
 // Register merge of row b by wave 0.  The row's N hot candidates sit in the
 // LDS list in no particular order (every step below is order independent);
 // slot t of lane l holds entry 64 t + l, so NS is ceil(N / 64) rounded up to
 // a compiled slot count.  The listing waves' per-lane partial sums are in
-// sm.acc, the summaries' share of the normaliser bounds in sm.zp.  Returns
-// the path code (0 done, 3 exact engine).
+// sm.acc, the summaries' share of the normaliser bounds in sm.zp.  Between
+// the filters and the draw it takes part in one workgroup barrier (every
+// other wave takes part in it too), after which wave 1's speculative token
+// is in sm.tok.  Returns the path code (0 done, 3 exact engine).
 template <int NS>
 __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const RowParams& rp, float m, float tcov, float ub,
                                           const HotList& hl, int N, MergeSmem& sm) {
@@ -1112,102 +1218,49 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
     st.w[t] = valid ? w : 0ull;
     st.al |= valid ? (1u << t) : 0u;
   }
-  // the exact masses and the level-0 draw buckets: one interleaved scan of
-  // the per-lane partials (lane 63 ends with the totals)
+  // the exact masses and the normaliser of the whole list: one interleaved
+  // scan of the per-lane partials (lane 63 ends with the totals)
   uint64_t acc[4] = {sm.acc[0][lane], sm.acc[1][lane], sm.acc[2][lane], sm.acc[3][lane]};
-  const uint64_t b0 = acc[3];
   wscan_incl_u64_k<4>(acc);
   st.m_all = lane_u64(acc[0], 63);
   st.m_cov = lane_u64(acc[1], 63);
   st.cached = true;
   const ZBounds zb = z_finish(sm.zp, st.m_all + lane_u64(acc[2], 63));
   const uint32_t al0 = st.al;
-  if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
+  const bool ok = run_filters(st, a, rp, m, tcov, zb);
+  const bool all_kept = __ballot(st.al != al0) == 0ull;
+  __syncthreads();  // wave 1's speculative token is in sm.tok
+  if (!ok) return 3;
 
   // Draw: integer inverse CDF in vocabulary order over the kept slots.
   const float invT = (float)(1.0 / (double)rp.T);
   const float Tc = (float)fmax((double)rp.T, 1e-5);
-  if (tscale) {
+  uint64_t ZV;
+  int tok = 0;
+  if (all_kept) {
+    ZV = lane_u64(acc[3], 63);
+    tok = sm.tok;
+  } else {
+    if (tscale) {
 #pragma unroll
-    for (int t = 0; t < NS; ++t) st.w[t] = st.on(t) ? wd[t] : 0ull;
-  }
-  // The draw is the smallest id whose inclusive kept weight, in vocabulary
-  // order, exceeds the target.  The candidates are in no order.  Level 0
-  // sums the kept weights of each block of 4096 ids (bucket d at lane d),
-  // scans the lanes and takes the first bucket whose inclusive sum exceeds
-  // the target; its scan total is the normaliser ZV.  When the filters kept
-  // every listed candidate, the listing waves' buckets are that sum already.
-  // Inside the chosen bucket, a handful of members is resolved directly:
-  // each member's inclusive weight over the members at or below its id,
-  // then the smallest id above the remaining target.  More members go
-  // through two more 6-bit radix levels.
-  const bool all_kept = __ballot(st.al != al0) == 0ull;
-  uint64_t incl0 = acc[3], bv0 = b0;
-  if (!all_kept) {
+      for (int t = 0; t < NS; ++t) st.w[t] = st.on(t) ? wd[t] : 0ull;
+    }
     sm.bucket[0][lane] = 0;
     wave_sync();
 #pragma unroll
     for (int t = 0; t < NS; ++t)
       if (st.on(t)) atomicAdd((unsigned long long*)&sm.bucket[0][(uint32_t)st.ci[t] >> 12], (unsigned long long)st.w[t]);
     wave_sync();
-    bv0 = sm.bucket[0][lane];
-    incl0 = wscan_incl_u64(bv0);
-  }
-  const uint64_t ZV = lane_u64(incl0, 63);
-  int tok = 0;
-  if (a.tokens && ZV) {
-    uint64_t rem = draw_target(ub, ZV);
-    // a bucket exists: rem is below the total
-    const int p0 = (int)__ffsll((long long)__ballot(incl0 > rem)) - 1;
-    rem -= lane_u64(incl0, p0) - lane_u64(bv0, p0);
-    auto member = [&](int t) { return st.on(t) && ((uint32_t)st.ci[t] >> 12) == (uint32_t)p0; };
-    int nmem = 0;
-#pragma unroll
-    for (int t = 0; t < NS; ++t) nmem += ballot_count(member(t));
-    if (nmem <= DRAW_MEMBERS) {
-      uint64_t cum[NS];
-#pragma unroll
-      for (int t = 0; t < NS; ++t) cum[t] = 0;
-#pragma unroll
-      for (int t = 0; t < NS; ++t) {
-        uint64_t bits = __ballot(member(t));
-        while (bits) {
-          const int k = (int)__builtin_ctzll(bits);
-          bits &= bits - 1;
-          const uint32_t idk = lane_u32((uint32_t)st.ci[t], k);
-          const uint64_t wk = lane_u64(st.w[t], k);
-#pragma unroll
-          for (int q = 0; q < NS; ++q) cum[q] += (uint32_t)st.ci[q] >= idk ? wk : 0ull;
-        }
-      }
-      uint32_t best = 0xFFFFFFFFu;
-#pragma unroll
-      for (int t = 0; t < NS; ++t)
-        if (member(t) && cum[t] > rem) best = min(best, (uint32_t)st.ci[t]);
-      tok = (int)wmin_u32(best);
-    } else {
-      uint32_t prefix = (uint32_t)p0;
-      sm.bucket[1][lane] = 0;
-      sm.bucket[2][lane] = 0;
-      wave_sync();
-      for (int lev = 1; lev < 3; ++lev) {
-        const int sh = 12 - 6 * lev;
-#pragma unroll
-        for (int t = 0; t < NS; ++t) {
-          if (st.on(t) && ((uint32_t)st.ci[t] >> (sh + 6)) == prefix)
-            atomicAdd((unsigned long long*)&sm.bucket[lev][((uint32_t)st.ci[t] >> sh) & 63u], (unsigned long long)st.w[t]);
-        }
-        wave_sync();
-        const uint64_t bv = sm.bucket[lev][lane];
-        const uint64_t incl = wscan_incl_u64(bv);
-        const int bsel = (int)__ffsll((long long)__ballot(incl > rem)) - 1;
-        rem -= lane_u64(incl, bsel) - lane_u64(bv, bsel);
-        prefix = (prefix << 6) | (uint32_t)bsel;
-      }
-      tok = (int)prefix;
+    const uint64_t bv0 = sm.bucket[0][lane];
+    const uint64_t incl0 = wscan_incl_u64(bv0);
+    ZV = lane_u64(incl0, 63);
+    if (a.tokens && ZV) {
+      uint64_t rem;
+      const int p0 = draw_level0(incl0, bv0, ZV, ub, rem);
+      tok = draw_in_block<NS>(st.ci, st.w, st.al, p0, rem, sm);
     }
   }
-  if (a.tokens && lane == 0) a.tokens[b] = tok;
+  if (a.tokens && lane == 0) a.tokens[b] = ZV ? tok : 0;
   if (a.kept) {
     const int nkept = st.count();
     if (lane == 0) a.kept[b] = nkept;
@@ -1427,8 +1480,19 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
       if (lane == 0) sm.zp = zp;
     }
     __syncthreads();
-    if (wv == 0) {
-      const int N = sm.n;
+    const int N = sm.n;
+    if (wv != 0) {
+      // wave 1 draws over the whole list meanwhile; every wave then meets
+      // wave 0 at the barrier between its filters and its draw
+      if (wv == 1 && a.tokens) {
+        if (N <= 64) spec_draw<1>(tscale, ub, hl, N, sm);
+        else if (N <= 128) spec_draw<2>(tscale, ub, hl, N, sm);
+        else if (N <= 256) spec_draw<4>(tscale, ub, hl, N, sm);
+        else if (N <= 512) spec_draw<8>(tscale, ub, hl, N, sm);
+        else spec_draw<QM>(tscale, ub, hl, N, sm);
+      }
+      __syncthreads();
+    } else {
       if (N <= 64) path = merge_regs<1>(a, b, rp, m, tcov, ub, hl, N, sm);
       else if (N <= 128) path = merge_regs<2>(a, b, rp, m, tcov, ub, hl, N, sm);
       else if (N <= 256) path = merge_regs<4>(a, b, rp, m, tcov, ub, hl, N, sm);
