@@ -1189,17 +1189,39 @@ __device__ __forceinline__ void spec_draw(bool tscale, float ub, const HotList& 
   if (lane == 0) sm.tok = tok;
 }
 
+// The filters' outcome from the totals alone, for chains where min-p is the
+// last filter on the listed candidates and there is no top-k: the listed
+// candidates all reach thr, so min-p keeps them all, and top-p (the same
+// steps as run_filters) either keeps every listed candidate (0), sends the
+// row to the exact engine (3), or needs the candidates themselves (-1: a cut
+// inside the list, or nothing kept).
+__device__ __forceinline__ int quick_filters(const RowParams& rp, ZBounds zb, uint64_t m_cov) {
+  if (!rp.use_p) return 0;
+  if (zb.lo > zb.hi) return 3;
+  const float theta = (float)(1.0 - (double)rp.top_p);
+  const long long Rlo = (long long)(zb.lo - floor_theta_z(theta, zb.lo));
+  const long long Rhi = (long long)(zb.hi - floor_theta_z(theta, zb.hi));
+  if (Rhi <= 0) return -1;
+  if (Rlo <= 0) return 3;
+  const long long Scov = (long long)m_cov;
+  if (Rlo > Scov) return rp.tp ? 3 : 0;
+  if (Rhi > Scov) return 3;
+  return -1;
+}
+
 // Register merge of row b by wave 0.  The row's N hot candidates sit in the
 // LDS list in no particular order (every step below is order independent);
 // slot t of lane l holds entry 64 t + l, so NS is ceil(N / 64) rounded up to
 // a compiled slot count.  The listing waves' per-lane partial sums are in
-// sm.acc, the summaries' share of the normaliser bounds in sm.zp.  Between
-// the filters and the draw it takes part in one workgroup barrier (every
-// other wave takes part in it too), after which wave 1's speculative token
-// is in sm.tok.  Returns the path code (0 done, 3 exact engine).
+// m_all / m_cov are the list's exact mass and its mass at or above tcov, ZV
+// its total draw weight, zb the row's normaliser bounds.  Between the
+// filters and the draw it takes part in one workgroup barrier (every other
+// wave takes part in it too), after which wave 1's speculative token is in
+// sm.tok.  Returns the path code (0 done, 3 exact engine).
 template <int NS>
 __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const RowParams& rp, float m, float tcov, float ub,
-                                          const HotList& hl, int N, MergeSmem& sm) {
+                                          const HotList& hl, int N, uint64_t m_all, uint64_t m_cov, uint64_t ZV_all,
+                                          ZBounds zb, MergeSmem& sm) {
   const int lane = threadIdx.x & 63;
   const bool tscale = rp.T != 1.0f;
   RegStore<NS> st;
@@ -1218,14 +1240,9 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
     st.w[t] = valid ? w : 0ull;
     st.al |= valid ? (1u << t) : 0u;
   }
-  // the exact masses and the normaliser of the whole list: one interleaved
-  // scan of the per-lane partials (lane 63 ends with the totals)
-  uint64_t acc[4] = {sm.acc[0][lane], sm.acc[1][lane], sm.acc[2][lane], sm.acc[3][lane]};
-  wscan_incl_u64_k<4>(acc);
-  st.m_all = lane_u64(acc[0], 63);
-  st.m_cov = lane_u64(acc[1], 63);
+  st.m_all = m_all;
+  st.m_cov = m_cov;
   st.cached = true;
-  const ZBounds zb = z_finish(sm.zp, st.m_all + lane_u64(acc[2], 63));
   const uint32_t al0 = st.al;
   const bool ok = run_filters(st, a, rp, m, tcov, zb);
   const bool all_kept = __ballot(st.al != al0) == 0ull;
@@ -1238,7 +1255,7 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
   uint64_t ZV;
   int tok = 0;
   if (all_kept) {
-    ZV = lane_u64(acc[3], 63);
+    ZV = ZV_all;
     tok = sm.tok;
   } else {
     if (tscale) {
@@ -1493,11 +1510,28 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
       }
       __syncthreads();
     } else {
-      if (N <= 64) path = merge_regs<1>(a, b, rp, m, tcov, ub, hl, N, sm);
-      else if (N <= 128) path = merge_regs<2>(a, b, rp, m, tcov, ub, hl, N, sm);
-      else if (N <= 256) path = merge_regs<4>(a, b, rp, m, tcov, ub, hl, N, sm);
-      else if (N <= 512) path = merge_regs<8>(a, b, rp, m, tcov, ub, hl, N, sm);
-      else path = merge_regs<QM>(a, b, rp, m, tcov, ub, hl, N, sm);
+      // the exact masses and the normaliser of the whole list: one
+      // interleaved scan of the per-lane partials (lane 63 ends with the
+      // totals)
+      uint64_t acc[4] = {sm.acc[0][lane], sm.acc[1][lane], sm.acc[2][lane], sm.acc[3][lane]};
+      wscan_incl_u64_k<4>(acc);
+      const uint64_t m_all = lane_u64(acc[0], 63), m_cov = lane_u64(acc[1], 63), ZV = lane_u64(acc[3], 63);
+      const ZBounds zb = z_finish(sm.zp, m_all + lane_u64(acc[2], 63));
+      // with min-p last and no top-k the totals settle most rows: then the
+      // candidates need not be loaded at all
+      const int quick = (rp.use_m && !rp.use_k && !a.out_rows) ? quick_filters(rp, zb, m_cov) : -1;
+      if (quick >= 0) {
+        __syncthreads();  // wave 1's speculative token is in sm.tok
+        path = quick;
+        if (quick == 0 && lane == 0) {
+          if (a.tokens) a.tokens[b] = ZV ? sm.tok : 0;
+          if (a.kept) a.kept[b] = N;
+        }
+      } else if (N <= 64) path = merge_regs<1>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+      else if (N <= 128) path = merge_regs<2>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+      else if (N <= 256) path = merge_regs<4>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+      else if (N <= 512) path = merge_regs<8>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+      else path = merge_regs<QM>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
       if (lane == 0) {
         s_path = path;
         P.path[b] = path;
