@@ -258,24 +258,6 @@ __device__ __forceinline__ uint32_t wscan_incl_u32(uint32_t x) {
   return x;
 }
 
-// K independent inclusive scans interleaved (as wsum_u64_k): lane 63 ends
-// with each total.
-template <int K>
-__device__ __forceinline__ void wscan_incl_u64_k(uint64_t (&v)[K]) {
-#define WH_SCANK_STEP(C, ROWS)                                                                              \
-  _Pragma("unroll") for (int k_ = 0; k_ < K; ++k_) {                                                        \
-    const uint64_t y_ = ((uint64_t)dpp32z<C, ROWS>((uint32_t)(v[k_] >> 32)) << 32) | dpp32z<C, ROWS>((uint32_t)v[k_]); \
-    v[k_] += y_;                                                                                            \
-  }
-  WH_SCANK_STEP(0x111, 0xF)
-  WH_SCANK_STEP(0x112, 0xF)
-  WH_SCANK_STEP(0x114, 0xF)
-  WH_SCANK_STEP(0x118, 0xF)
-  WH_SCANK_STEP(0x142, 0xA)
-  WH_SCANK_STEP(0x143, 0xC)
-#undef WH_SCANK_STEP
-}
-
 // Number of lanes (of the active ones) where p holds; wave uniform.
 __device__ __forceinline__ int ballot_count(bool p) { return (int)__popcll(__ballot(p)); }
 

@@ -1189,6 +1189,28 @@ __device__ __forceinline__ void spec_draw(bool tscale, float ub, const HotList& 
   if (lane == 0) sm.tok = tok;
 }
 
+// Totals of the four 64-entry per-lane sums in LDS: lanes 16k..16k+15 add
+// four entries of array k each, the four DPP steps inside a row of 16
+// (dpp_reduce_u64's first four) finish each row, and lane 16k holds array
+// k's total.
+__device__ __forceinline__ void totals4(const uint64_t (*acc)[64], uint64_t (&t)[4]) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t* p = &acc[lane >> 4][(lane & 15) * 4];
+  uint64_t x = (p[0] + p[1]) + (p[2] + p[3]);
+#define WH_ROW_STEP(C)                                                                          \
+  {                                                                                             \
+    const uint64_t y_ = ((uint64_t)dpp32<C>((uint32_t)(x >> 32)) << 32) | dpp32<C>((uint32_t)x); \
+    x += y_;                                                                                    \
+  }
+  WH_ROW_STEP(0xB1)
+  WH_ROW_STEP(0x4E)
+  WH_ROW_STEP(0x141)
+  WH_ROW_STEP(0x140)
+#undef WH_ROW_STEP
+#pragma unroll
+  for (int k = 0; k < 4; ++k) t[k] = lane_u64(x, 16 * k);
+}
+
 // The filters' outcome from the totals alone, for chains where min-p is the
 // last filter on the listed candidates and there is no top-k: the listed
 // candidates all reach thr, so min-p keeps them all, and top-p (the same
@@ -1510,13 +1532,11 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
       }
       __syncthreads();
     } else {
-      // the exact masses and the normaliser of the whole list: one
-      // interleaved scan of the per-lane partials (lane 63 ends with the
-      // totals)
-      uint64_t acc[4] = {sm.acc[0][lane], sm.acc[1][lane], sm.acc[2][lane], sm.acc[3][lane]};
-      wscan_incl_u64_k<4>(acc);
-      const uint64_t m_all = lane_u64(acc[0], 63), m_cov = lane_u64(acc[1], 63), ZV = lane_u64(acc[3], 63);
-      const ZBounds zb = z_finish(sm.zp, m_all + lane_u64(acc[2], 63));
+      // the exact masses and the normaliser of the whole list
+      uint64_t tot[4];
+      totals4(sm.acc, tot);
+      const uint64_t m_all = tot[0], m_cov = tot[1], ZV = tot[3];
+      const ZBounds zb = z_finish(sm.zp, m_all + tot[2]);
       // with min-p last and no top-k the totals settle most rows: then the
       // candidates need not be loaded at all
       const int quick = (rp.use_m && !rp.use_k && !a.out_rows) ? quick_filters(rp, zb, m_cov) : -1;
