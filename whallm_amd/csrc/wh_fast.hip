@@ -388,7 +388,9 @@ __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logi
   constexpr int ESZ = DT ? 2 : 4;
   constexpr uint32_t NEG = DT ? 0xFF80FF80u : 0xFF800000u;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int b = blockIdx.x / G, s = blockIdx.x - b * G;
+  // grid (G, B): workgroup (s, b) is slice s of row b; the linear order
+  // (s fastest) is the dispatch order
+  const int b = blockIdx.y, s = blockIdx.x;
   const int v0 = s * SL, v1 = min(V, v0 + SL);
 
   // 1. loads, in the order they are needed: the history window (up to 4 ids
@@ -1642,7 +1644,7 @@ static int launch_slice_t(const SampleKArgs& k, const FastPlan& fp, size_t lds, 
   auto fn = slice_kernel<DT, R>;
   int rc = set_lds((const void*)fn, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(fn, dim3(k.B * fp.G), dim3(FT), lds, st, (const char*)k.logits, k.hist, (long long)k.row_stride, fp.G,
+  hipLaunchKernelGGL(fn, dim3(fp.G, k.B), dim3(FT), lds, st, (const char*)k.logits, k.hist, (long long)k.row_stride, fp.G,
                      fp.SL, k.V, (int)k.hist_stride, k.hcap > 0 ? 1 : 0, k, fp);
   return WH_OK;
 }
