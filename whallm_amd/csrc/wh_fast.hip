@@ -922,6 +922,14 @@ struct RegStore {
       target -= lane_u64(incl, sel) - lane_u64(bv, sel);
       prefix = (prefix << 6) | (uint64_t)(63 - sel);
       wave_sync();
+      // counting, a chosen bucket of count one is the answer: the target lies
+      // inside that bucket's measure
+      if (!MASS && sh > 0 && lane_u64(bv, sel) == 1ull) {
+        uint64_t only = 0;
+#pragma unroll
+        for (int t = 0; t < NS; ++t) only |= (on(t) && f(t) && (c[t] >> sh) == prefix) ? c[t] : 0ull;
+        return dpp_reduce_u64(only, [](uint64_t x, uint64_t y) { return x | y; });
+      }
     }
     return prefix;
   }
