@@ -138,6 +138,45 @@ def test_random_parameters_parity(S, dev, oracle, seed):
         assert np.array_equal(tok, ot), engine
 
 
+@pytest.mark.parametrize("seed", range(3))
+def test_dense_block_and_ties_full_vocab(S, dev, oracle, seed):
+    """Full-vocabulary rows built to reach the rarer steps of the register
+    merge: hundreds of near-max candidates inside one 4096-id block (the
+    draw's block has more than 16 members, so both the speculative and the
+    filtered draw take the radix levels), rows of exact ties under top-k
+    (a radix bucket of count one ends the select early only when it is
+    unique), and a temperature != 1 so the draw weights differ from the
+    masses."""
+    rng = np.random.default_rng(700 + seed)
+    B, V = 24, 151936
+    x = rng.normal(0, 1.5, (B, V)).astype(np.float32) - 6.0
+    for r in range(B):
+        kind = r % 3
+        if kind == 0:   # a dense block of near-max candidates
+            blk = int(rng.integers(0, V // 4096)) * 4096
+            ids = blk + rng.choice(4096, 300, replace=False)
+            x[r, ids] = rng.uniform(2.0, 2.4, 300).astype(np.float32)
+        elif kind == 1:  # exact ties around the k-th value
+            ids = rng.choice(V, 64, replace=False)
+            x[r, ids] = np.float32(3.0)
+            x[r, ids[:5]] = np.float32(3.5)
+        else:            # a few clear leaders and a tied tail
+            ids = rng.choice(V, 40, replace=False)
+            x[r, ids] = np.round(rng.uniform(1.0, 3.0, 40) * 4).astype(np.float32) / 4
+    u = rng.random(B, dtype=np.float32)
+    cases = [dict(temperature=0.7, top_p=0.9, top_k=0, min_p=0.05, chain=1),
+             dict(temperature=1.3, top_p=1.0, top_k=20, min_p=0.0, chain=0),
+             dict(temperature=0.8, top_p=0.95, top_k=7, min_p=0.02, chain=1)]
+    for c in cases:
+        p = oracle.make_params(B, **c)
+        ot, ok = oracle.sample(x, p, u)
+        announce(f"wh_sample dense-block/ties seed={seed} B={B} V={V} {c}")
+        tok, kept = S.sample(torch.from_numpy(x).to(dev), uniforms=torch.from_numpy(u).to(dev), return_kept=True, **c)
+        tok, kept = tok.cpu().numpy(), kept.cpu().numpy()
+        assert np.array_equal(kept, ok), c
+        assert np.array_equal(tok, ot), c
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_per_row_parameters_parity(S, dev, oracle, seed):
     rng = np.random.default_rng(200 + seed)
