@@ -545,18 +545,22 @@ __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logi
   // -inf); with penalties, the marked elements are swapped out first
   float gm[R];
   float mx = -INFINITY;
+  if (pen) {
+    // branch-free, so every group's code read issues back to back (a group
+    // past the slice reads the first codes and is overwritten below)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int g = v0 + (r * FT + tid) * EPT;
+      const uint4 cw = *(const uint4*)(codes + (size_t)(g < v1 ? g - v0 : 0) * ESZ);
+      d[r].x |= cw.x;
+      d[r].y |= cw.y;
+      d[r].z |= cw.z;
+      d[r].w |= cw.w;
+    }
+  }
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int g = v0 + (r * FT + tid) * EPT;
-    if (pen && g < v1) {
-      const uint4 cw = *(const uint4*)(codes + (size_t)(g - v0) * ESZ);
-      if ((cw.x | cw.y | cw.z | cw.w) != 0u) {
-        d[r].x |= cw.x;
-        d[r].y |= cw.y;
-        d[r].z |= cw.z;
-        d[r].w |= cw.w;
-      }
-    }
     if (g >= v1) d[r] = make_uint4(NEG, NEG, NEG, NEG);
     gm[r] = grp_max<DT>(d[r]);
     mx = fmaxf(mx, gm[r]);
