@@ -937,9 +937,9 @@ struct RegStore {
     }
     return prefix;
   }
-  // Top-k in order A (value desc, id asc) over the alive slots.
+  // Top-k in order A (value desc, id asc) over the alive slots; the caller
+  // has checked that more than k are alive.
   __device__ __forceinline__ void keep_topk(int k) {
-    if (count() <= k) return;
     const uint64_t ck = select_desc<ORD_A, false>([](int) { return true; }, (uint64_t)k, bkt);
     keep_if([&](int t) { return comp_a(fkey(cl[t]), ci[t]) >= ck; });
   }
@@ -1009,9 +1009,9 @@ struct BlockStore {
     pr.use_m = 1;
     pr.thr = thr;
   }
+  // the caller has checked that more than k are kept
   __device__ __forceinline__ void keep_topk(int k) {
-    if (count() <= k) return;
-    const uint64_t ck = radix_select<ORD_A, true>(src, pr, [](int, float) { return (uint64_t)1; }, (uint64_t)k, *sm);
+    const uint64_t ck = radix_select<ORD_A, true, true>(src, pr, [](int, float) { return (uint64_t)1; }, (uint64_t)k, *sm);
     pr.use_k = 1;
     pr.ck = ck;
   }
@@ -1069,7 +1069,7 @@ __device__ __forceinline__ bool run_filters(St& st, const SampleKArgs& a, const 
   const float thr = m + min_p_log(a, rp.min_p);
   if (a.chain == WH_CHAIN_MLX && rp.use_k && rp.use_p) {
     // k -> p -> min-p; the candidates hold the whole top-k set
-    st.keep_topk(rp.top_k);
+    if (st.count() > rp.top_k) st.keep_topk(rp.top_k);
     if (!apply_p(true)) return false;
     if (!none && rp.use_m) st.keep_min(thr);
   } else {
@@ -1377,13 +1377,28 @@ __device__ __noinline__ int merge_block(const SampleKArgs* ap, const FastPlan* p
       ++nk;
     }
   });
-  const uint64_t ZV = block_reduce(zv, sm.scratch64, OpSumU64(), (uint64_t)0);
-  const int nkept = block_reduce(nk, sm.scratchi, OpSumI(), 0);
+  // the two sums in one block reduction (one pair of barriers)
+  const int lane = tid & 63, wv = tid >> 6, nw = nt >> 6;
+  zv = wsum_u64(zv);
+  nk = wsum_i(nk);
+  __syncthreads();
+  if (lane == 0) {
+    sm.scratch64[wv] = zv;
+    sm.scratchi[wv] = nk;
+  }
+  __syncthreads();
+  uint64_t ZV = 0;
+  int nkept = 0;
+  for (int w = 0; w < nw; ++w) {
+    ZV += sm.scratch64[w];
+    nkept += sm.scratchi[w];
+  }
   if (a.tokens) {
     int tok = 0;
     if (ZV) {
       const uint64_t tgt = draw_target(ub, ZV);
-      tok = 0x3FFFF - (int)radix_select<ORD_ID, true>(src, pr, vw, tgt + 1, sm);
+      // ids have 18 bits: two 10-bit passes, no common-prefix pass
+      tok = 0x3FFFF - (int)radix_select<ORD_ID>(src, pr, vw, tgt + 1, sm);
     }
     if (tid == 0) a.tokens[b] = tok;
   }
