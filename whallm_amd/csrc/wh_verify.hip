@@ -300,6 +300,9 @@ constexpr int VT2 = 1024;      // threads, passes 2 and 3
 constexpr int VG2MAX = 16;     // slices of the selected row
 constexpr int VSEG4 = 2;       // float4 groups per thread in the final draw (1024 threads: 8192 ids)
 constexpr double VEPS = 2e-4;  // relative slack of the float normaliser
+// slices of the selected row hold at most 4 * VSEG4 * VT2 ids: the prep and
+// residual passes read them as 2 float4 per thread
+static_assert(VSEG4 == 2 && VT2 == 1024, "sliced verify: 2 float4 per thread cover a slice");
 
 struct VRowSum {
   float m;
@@ -356,52 +359,70 @@ __global__ void __launch_bounds__(VT1) verify_sum_kernel(VerifyKArgs a, VPlan P)
 
 // Row j of batch entry b from the slice summaries: the max, and the proven
 // interval of the fixed-point normaliser.
-__device__ void vrow_bounds(const VerifyKArgs& a, const VPlan& P, int b, int j, float* m_out, uint64_t* zlo,
-                            uint64_t* zhi) {
-  const VRowSum* rs = P.summ + ((long long)b * (a.n + 1) + j) * P.G1;
+__device__ void vrow_bounds_of(const VRowSum* rs, int G1, float Tc, int V, float* m_out, uint64_t* zlo,
+                               uint64_t* zhi) {
   float m = -INFINITY;
-  for (int s = 0; s < P.G1; ++s) m = fmaxf(m, rs[s].m);
+  for (int s = 0; s < G1; ++s) m = fmaxf(m, rs[s].m);
   // the float rescale's relative error (a few ulp) is far inside VEPS
   double zf = 0.0;
   if (m != -INFINITY)
-    for (int s = 0; s < P.G1; ++s)
-      if (rs[s].m != -INFINITY) zf += rs[s].zf * (double)__expf((rs[s].m - m) / a.Tc);
+    for (int s = 0; s < G1; ++s)
+      if (rs[s].m != -INFINITY) zf += rs[s].zf * (double)__expf((rs[s].m - m) / Tc);
   const double SC = 17592186044416.0, LIM = 4.0e18;
-  const double lo = zf * SC * (1.0 - VEPS) - (double)a.V, hi = zf * SC * (1.0 + VEPS) + (double)a.V;
+  const double lo = zf * SC * (1.0 - VEPS) - (double)V, hi = zf * SC * (1.0 + VEPS) + (double)V;
   *m_out = m;
   *zlo = (m == -INFINITY || lo <= 0.0) ? 0ull : (uint64_t)lo;
   *zhi = m == -INFINITY ? 0ull : (hi >= LIM ? (1ull << 62) : (uint64_t)ceil(hi));
 }
 
-// Row j's max from the slice summaries.
-__device__ __forceinline__ float vrow_max(const VerifyKArgs& a, const VPlan& P, int b, int j) {
+// Wave-level reads (every lane of a full wave calls them): lane s reads one
+// row summary or one partial sum, so the reads are a single round trip, and
+// DPP reductions finish them; every lane gets the result.
+//  * row j's max from its G1 <= 8 slice summaries;
+//  * the sum of cnt <= 64 per-slice partial sums.
+__device__ __forceinline__ float vrow_max_w(const VerifyKArgs& a, const VPlan& P, int b, int j) {
+  const int lane = threadIdx.x & 63;
   const VRowSum* rs = P.summ + ((long long)b * (a.n + 1) + j) * P.G1;
-  float m = -INFINITY;
-  for (int s = 0; s < P.G1; ++s) m = fmaxf(m, rs[s].m);
-  return m;
+  return wmax_f(lane < P.G1 ? rs[lane].m : -INFINITY);
+}
+__device__ __forceinline__ uint64_t vparts_sum_w(const unsigned long long* p, int cnt) {
+  const int lane = threadIdx.x & 63;
+  return wsum_u64(lane < cnt ? (uint64_t)p[lane] : 0ull);
 }
 
 __global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P) {
   __shared__ VSmem sm;
   __shared__ int s_state[64];
+  __shared__ float s_m[64];
+  __shared__ VRowSum s_rs[64 * 8];  // rows j < n (n < 64), G1 <= 8 summaries each
   const int tid = threadIdx.x;
   const int b = blockIdx.x / P.G2, s = blockIdx.x - b * P.G2;
-  const int n = a.n, V = a.V;
+  const int n = a.n, V = a.V, G1 = P.G1;
+  // Every summary of rows j < n in one round trip, staged in LDS (rows of
+  // one batch entry are contiguous), with each row's draft token and uniform
+  // read alongside.
+  for (int k = tid; k < n * G1; k += VT2) s_rs[k] = P.summ[(long long)b * (n + 1) * G1 + k];
+  int tk = 0;
+  float u = 0.0f;
+  if (tid < n) {
+    tk = a.tok[(long long)b * n + tid];
+    u = a.u[(long long)b * (n + 1) + tid];
+  }
+  __syncthreads();
   // decisions: 0 accept, 1 reject, 2 undecided by the bounds
   if (tid < n) {
     const int j = tid;
-    const int tk = a.tok[(long long)b * n + j];
     float m;
     uint64_t zlo, zhi;
-    vrow_bounds(a, P, b, j, &m, &zlo, &zhi);
+    vrow_bounds_of(s_rs + j * G1, G1, a.Tc, V, &m, &zlo, &zhi);
+    s_m[j] = m;
     int st;
     if (tk < 0 || tk >= V) {
       st = 1;
     } else {
       const float xt = a.target[((long long)b * (n + 1) + j) * V + tk];
-      const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(xt, m, a.Tc));
       const float q = a.draft[((long long)b * n + j) * V + tk];
-      const float u = a.u[(long long)b * (n + 1) + j];
+      const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(xt, m, a.Tc));
       if (reject_fused(u, q, zlo, W)) st = 1;
       else if (!reject_fused(u, q, zhi, W)) st = 0;
       else st = 2;
@@ -427,17 +448,27 @@ __global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P
   __syncthreads();
   const int js = sm.bcasti[0];
   if (sm.bcasti[1]) return;
-  const float m = vrow_max(a, P, b, js);
   const float* x = a.target + ((long long)b * (n + 1) + js) * V;
   const int v0 = s * P.SL2, v1 = min(V, v0 + P.SL2);
+  // the slice (at most 2 float4 per thread: SL2 <= 8192) is read before the
+  // row max is needed; positions past the slice (the slice may be empty) read
+  // the row's first float4 and are ignored
+  float4 c[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = v0 + (tid + k * VT2) * 4;
+    c[k] = *(const float4*)(x + (i < v1 ? i : 0));
+  }
+  const float m = js < n ? s_m[js] : vrow_max_w(a, P, b, js);
   uint64_t z = 0;
-  if (m != -INFINITY)
-#pragma unroll 4
-    for (int i = v0 + tid * 4; i < v1; i += VT2 * 4) {
-      const float4 c = *(const float4*)(x + i);
-      z += exp_fix44(vweight_arg(c.x, m, a.Tc)) + exp_fix44(vweight_arg(c.y, m, a.Tc));
-      z += exp_fix44(vweight_arg(c.z, m, a.Tc)) + exp_fix44(vweight_arg(c.w, m, a.Tc));
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = v0 + (tid + k * VT2) * 4;
+    if (m != -INFINITY && i < v1) {
+      z += exp_fix44(vweight_arg(c[k].x, m, a.Tc)) + exp_fix44(vweight_arg(c[k].y, m, a.Tc));
+      z += exp_fix44(vweight_arg(c[k].z, m, a.Tc)) + exp_fix44(vweight_arg(c[k].w, m, a.Tc));
     }
+  }
   const uint64_t zt = block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
   if (tid == 0) P.zpart[(long long)b * P.G2 + s] = zt;
 }
@@ -449,23 +480,31 @@ __global__ void __launch_bounds__(VT2) verify_resid_kernel(VerifyKArgs a, VPlan 
   const int n = a.n, V = a.V;
   const int js = P.jst[2 * b];
   if (P.jst[2 * b + 1] || js >= n) return;
-  uint64_t Z = 0;
-  for (int t = 0; t < P.G2; ++t) Z += P.zpart[(long long)b * P.G2 + t];
-  const float m = vrow_max(a, P, b, js);
   const float* x = a.target + ((long long)b * (n + 1) + js) * V;
   const float* q = a.draft + ((long long)b * n + js) * V;
   const int v0 = s * P.SL2, v1 = min(V, v0 + P.SL2);
+  // the slice (at most 2 float4 of each row per thread), the partial sums
+  // and the summaries are all read in one round trip; positions past the
+  // slice read the row's first float4 and are ignored
+  float4 c[2], d[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = v0 + (tid + k * VT2) * 4, ic = i < v1 ? i : 0;
+    c[k] = *(const float4*)(x + ic);
+    d[k] = *(const float4*)(q + ic);
+  }
+  const uint64_t Z = vparts_sum_w(P.zpart + (long long)b * P.G2, P.G2);
+  const float m = vrow_max_w(a, P, b, js);
   uint64_t r = 0;
   auto res = [&](float xv, float qv) {
     const uint64_t w = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(xv, m, a.Tc));
     const uint64_t qz = floor_qz(qv, Z);
     return w > qz ? w - qz : (uint64_t)0;
   };
-#pragma unroll 4
-  for (int i = v0 + tid * 4; i < v1; i += VT2 * 4) {
-    const float4 c = *(const float4*)(x + i);
-    const float4 d = *(const float4*)(q + i);
-    r += res(c.x, d.x) + res(c.y, d.y) + res(c.z, d.z) + res(c.w, d.w);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = v0 + (tid + k * VT2) * 4;
+    if (i < v1) r += res(c[k].x, d[k].x) + res(c[k].y, d[k].y) + res(c[k].z, d[k].z) + res(c[k].w, d[k].w);
   }
   const uint64_t rt = block_reduce(r, sm.scratch64, OpSumU64(), (uint64_t)0);
   if (tid == 0) P.rpart[(long long)b * P.G2 + s] = rt;
@@ -579,29 +618,27 @@ __global__ void __launch_bounds__(1024) verify_pick_kernel(VerifyKArgs a, VPlan 
     verify_exact_entry(a, b, sm);
     return;
   }
-  uint64_t Z = 0, R = 0;
-  for (int t = 0; t < P.G2; ++t) {
-    Z += P.zpart[(long long)b * P.G2 + t];
-    if (js < n) R += P.rpart[(long long)b * P.G2 + t];
-  }
+  // lane t holds slice t's partial sums (one round trip); DPP sums and a
+  // scan over the lanes pick the slice
+  const int lane = tid & 63;
+  const bool ls = lane < P.G2;
+  const uint64_t zp = ls ? (uint64_t)P.zpart[(long long)b * P.G2 + lane] : 0ull;
+  const uint64_t rp = (ls && js < n) ? (uint64_t)P.rpart[(long long)b * P.G2 + lane] : 0ull;
+  const float ub = a.u[(long long)b * (n + 1) + n];
+  const float m = vrow_max_w(a, P, b, js);
+  const uint64_t Z = wsum_u64(zp), R = wsum_u64(rp);
   // residual mass when rejected and positive, else the row's own weights
   const bool use_r = js < n && R > 0;
-  const unsigned long long* parts = (use_r ? P.rpart : P.zpart) + (long long)b * P.G2;
+  const uint64_t part = use_r ? rp : zp;
   const uint64_t total = use_r ? R : Z;
+  const uint64_t incl = wscan_incl_u64(part);
   int tok = 0;
   if (total) {
-    const uint64_t tgt = draw_target(a.u[(long long)b * (n + 1) + n], total);
-    uint64_t before = 0;
-    int ss = P.G2 - 1;
-    for (int t = 0; t < P.G2; ++t) {
-      if (before + parts[t] > tgt) {
-        ss = t;
-        break;
-      }
-      before += parts[t];
-    }
-    const uint64_t rem = tgt - before;
-    const float m = vrow_max(a, P, b, js);
+    const uint64_t tgt = draw_target(ub, total);
+    // the first slice whose inclusive sum exceeds the target (lane 63 holds
+    // the total, which does)
+    const int ss = (int)__ffsll((long long)__ballot(incl > tgt)) - 1;
+    const uint64_t rem = tgt - (lane_u64(incl, ss) - lane_u64(part, ss));
     const float* x = a.target + ((long long)b * (n + 1) + js) * V;
     const int v0 = ss * P.SL2, v1 = min(V, v0 + P.SL2);
     auto wt = [&](float xv) { return m == -INFINITY ? (uint64_t)0 : exp_fix44(vweight_arg(xv, m, a.Tc)); };
