@@ -59,7 +59,8 @@ __device__ __forceinline__ uint64_t mant24(float x, int* e) {
   return (uint64_t)ldexpf(fr, 24);
 }
 
-// floor(theta * Z) for float32 theta in [0,1), Z < 2^62 (exact).  theta =
+// floor(theta * Z) for float32 theta in [0,1] (NaN and negatives give 0,
+// larger values clamp to 1), Z < 2^62 (exact).  theta =
 // M 2^-s with a 24-bit M and s >= 23, so with Z = Zh 2^32 + Zl the product
 // M Z = hi 2^32 + lo (hi = M Zh < 2^54, lo = M Zl < 2^56) is shifted in two
 // 64-bit pieces: for s <= 32, hi 2^(32-s) is whole and only lo loses bits;

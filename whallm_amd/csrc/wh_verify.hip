@@ -56,16 +56,9 @@ __device__ __forceinline__ bool reject_lp(float u, float g, float d) {
   return (double)u * 17592186044416.0 > (double)R;
 }
 
-__device__ __forceinline__ uint64_t floor_qz(float q, uint64_t Z) {
-  if (!(q > 0.0f)) return 0;
-  if (q > 1.0f) q = 1.0f;
-  int e;
-  uint64_t M = mant24(q, &e);
-  int s = 24 - e;
-  u128 prod = (u128)M * Z;
-  u128 F = s >= 128 ? (u128)0 : (prod >> s);
-  return F > (u128)(~0ull) ? ~0ull : (uint64_t)F;
-}
+// floor(q Z) for q clamped to [0, 1] (so the result is at most Z): the same
+// two 64-bit products as floor_theta_z.
+__device__ __forceinline__ uint64_t floor_qz(float q, uint64_t Z) { return floor_theta_z(q, Z); }
 
 // reject iff u * q * Z > W (exact)
 __device__ __forceinline__ bool reject_fused(float u, float q, uint64_t Z, uint64_t W) {
