@@ -323,13 +323,16 @@ def test_verify_fused_workload3_full_size(S, dev, oracle):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("force_exact", [False, True])
-@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("seed", range(12))
 def test_verify_fused_sliced(S, dev, oracle, seed, force_exact, monkeypatch):
     """The sliced verifier (T > 0, V % 4 == 0): bounds-decided ratio tests,
     exact residual draw; with WH_VERIFY_FORCE_EXACT every entry takes the
-    exact per-row algorithm that undecided entries use."""
+    exact per-row algorithm that undecided entries use.  Seeds 10 and 11 use
+    long drafts (n = 17, 63: the most the sliced form takes)."""
     rng = np.random.default_rng(700 + seed)
     B, n = int(rng.integers(1, 20)), int(rng.integers(1, 11))
+    if seed >= 10:
+        B, n = int(rng.integers(1, 4)), (17, 63)[seed - 10]
     V = int(rng.choice([4096, 20000, 129280])) if seed < 8 else 129280
     T = float(rng.choice([0.3, 0.8, 1.0, 2.0]))
     x = rng.normal(0, 2.5, (B, n + 1, V)).astype(np.float32)

@@ -270,10 +270,12 @@ __global__ void __launch_bounds__(1024) verify_fused_draw_kernel(VerifyKArgs a) 
 
 // ---------------------------------------------------------------------------
 // Fused form, T > 0: sliced passes instead of one workgroup per row.
-//   1. verify_sum_kernel, one 512-thread workgroup per slice of every target
-//      row (several per CU): the slice's exact max and a float sum of
-//      exp((x - max) / T), streamed with a running max.  One HBM pass over
-//      the target rows.
+//   1. verify_sum_kernel, one 256-thread workgroup per slice of every target
+//      row (about eight per CU): the slice's exact max and a float sum of
+//      exp((x - max) / T), from loads that are all issued before any is used.
+//      One HBM pass over the target rows.  The first slice's workgroup also
+//      records the target logit and draft probability at the row's draft
+//      token.
 //   2. verify_prep_kernel, G2 workgroups per batch entry: each recomputes the
 //      accept / reject decisions from the row summaries -- the normaliser Z
 //      lies in [Zlo, Zhi] from the float sums, and u q Z > W is decided from
@@ -287,8 +289,11 @@ __global__ void __launch_bounds__(1024) verify_fused_draw_kernel(VerifyKArgs a) 
 //      decisions were not settled by the bounds runs the exact per-row
 //      algorithm here instead (identical results, slower).
 // ---------------------------------------------------------------------------
-constexpr int VT1 = 512;       // threads, pass 1
-constexpr int VE1 = 32768;     // elements per pass-1 slice, at most
+constexpr int VT1 = 256;       // threads, pass 1
+constexpr int VL1 = 8;         // float4 loads per thread, pass 1
+constexpr int VE1 = 4 * VL1 * VT1;  // elements per pass-1 slice, at most (8192)
+constexpr int VBLK1 = 2048;    // pass-1 workgroups aimed for (eight per CU)
+constexpr int VG1MAX = 64;     // pass-1 slices per row, at most (one wave lane each)
 constexpr int VT2 = 1024;      // threads, passes 2 and 3
 constexpr int VG2MAX = 16;     // slices of the selected row
 constexpr int VSEG4 = 2;       // float4 groups per thread in the final draw (1024 threads: 8192 ids)
@@ -296,6 +301,7 @@ constexpr double VEPS = 2e-4;  // relative slack of the float normaliser
 // slices of the selected row hold at most 4 * VSEG4 * VT2 ids: the prep and
 // residual passes read them as 2 float4 per thread
 static_assert(VSEG4 == 2 && VT2 == 1024, "sliced verify: 2 float4 per thread cover a slice");
+static_assert((WH_MAX_VOCAB + VE1 - 1) / VE1 <= VG1MAX, "pass-1 slices of a row fit one wave's lanes");
 
 struct VRowSum {
   float m;
@@ -303,11 +309,17 @@ struct VRowSum {
   double zf;  // sum of exp((x - m) / T) over the slice (hardware exp)
 };
 
+// The target logit and draft probability at row j's draft token.
+struct VTokRec {
+  float xt, q;
+};
+
 struct VPlan {
   int G1, SL1, G2, SL2;
   int force_exact;  // test hook: every batch entry takes the exact per-row algorithm
   VRowSum* summ;  // [B, n+1, G1]
-  int32_t* jst;   // [B, 2]: j*, undecided flag
+  VTokRec* trec;  // [B, n]
+  int32_t* jst;   // [B, 4]: j*, undecided flag, bits of row j*'s max, unused
   unsigned long long* zpart;  // [B, G2] exact weights of row j*
   unsigned long long* rpart;  // [B, G2] residual mass of row j*
 };
@@ -315,33 +327,66 @@ struct VPlan {
 __device__ __forceinline__ float vweight_arg(float x, float m, float Tc) { return (x - m) / Tc; }
 
 __global__ void __launch_bounds__(VT1) verify_sum_kernel(VerifyKArgs a, VPlan P) {
-  __shared__ VSmem sm;
-  const int tid = threadIdx.x;
+  __shared__ float s_m[VT1 / 64];
+  __shared__ double s_z[VT1 / 64];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int rj = blockIdx.x / P.G1, s = blockIdx.x - rj * P.G1;
-  const int V = a.V;
+  const int V = a.V, n = a.n;
   const int v0 = s * P.SL1, v1 = min(V, v0 + P.SL1);
   const float* row = a.target + (long long)rj * V;
-  const float iT = 1.0f / a.Tc;
-  // per thread: a running max and the float sum of exp((x - max) / T),
-  // rescaled whenever the max rises
-  float mt = -INFINITY, st = 0.0f;
-#pragma unroll 4
-  for (int i = v0 + tid * 4; i < v1; i += VT1 * 4) {
-    const float4 c = *(const float4*)(row + i);
-    const float cm = fmaxf(fmaxf(c.x, c.y), fmaxf(c.z, c.w));
-    if (cm > mt) {
-      st = mt == -INFINITY ? 0.0f : st * __expf((mt - cm) * iT);
-      mt = cm;
-    }
-    if (mt != -INFINITY) {
-      st += __expf((c.x - mt) * iT) + __expf((c.y - mt) * iT);
-      st += __expf((c.z - mt) * iT) + __expf((c.w - mt) * iT);
+  // every load of the thread is issued before any is used; positions past
+  // the slice (which may be empty) read the row's first float4 and are ignored
+  float4 c[VL1];
+#pragma unroll
+  for (int k = 0; k < VL1; ++k) {
+    const int i = v0 + (tid + k * VT1) * 4;
+    c[k] = *(const float4*)(row + (i < v1 ? i : 0));
+  }
+  // the first slice's workgroup records the draft token's logit and draft
+  // probability for the accept tests (rows j < n only)
+  const int b = rj / (n + 1), j = rj - b * (n + 1);
+  if (s == 0 && j < n && tid == 0) {
+    const int tk = a.tok[(long long)b * n + j];
+    if (tk >= 0 && tk < V) {
+      VTokRec r;
+      r.xt = row[tk];
+      r.q = a.draft[((long long)b * n + j) * V + tk];
+      P.trec[(long long)b * n + j] = r;
     }
   }
-  const float m = block_reduce(mt, sm.scratchf, OpMaxF(), -INFINITY);
-  const double zt = mt == -INFINITY ? 0.0 : (double)st * (double)__expf((mt - m) * iT);
-  const double zs = block_reduce(zt, sm.scratchd, OpSumF64(), 0.0);
+  float mt = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < VL1; ++k) {
+    const int i = v0 + (tid + k * VT1) * 4;
+    if (i < v1) mt = fmaxf(mt, fmaxf(fmaxf(c[k].x, c[k].y), fmaxf(c[k].z, c[k].w)));
+  }
+  mt = wmax_f(mt);
+  if (lane == 0) s_m[w] = mt;
+  __syncthreads();
+  float m = s_m[0];
+#pragma unroll
+  for (int k = 1; k < VT1 / 64; ++k) m = fmaxf(m, s_m[k]);
+  // exp((x - m) / T) = 2^((x - m) log2(e) / T), hardware exp2; the float
+  // sum of at most 32 terms per lane, then doubles
+  float st = 0.0f;
+  if (m != -INFINITY) {
+    const float k2 = 1.44269504088896341f / a.Tc;
+#pragma unroll
+    for (int k = 0; k < VL1; ++k) {
+      const int i = v0 + (tid + k * VT1) * 4;
+      if (i < v1) {
+        st += __builtin_amdgcn_exp2f((c[k].x - m) * k2) + __builtin_amdgcn_exp2f((c[k].y - m) * k2);
+        st += __builtin_amdgcn_exp2f((c[k].z - m) * k2) + __builtin_amdgcn_exp2f((c[k].w - m) * k2);
+      }
+    }
+  }
+  const double zw = wsum_f64((double)st);
+  if (lane == 0) s_z[w] = zw;
+  __syncthreads();
   if (tid == 0) {
+    double zs = 0.0;
+#pragma unroll
+    for (int k = 0; k < VT1 / 64; ++k) zs += s_z[k];
     VRowSum o;
     o.m = m;
     o.pad = 0.0f;
@@ -350,17 +395,15 @@ __global__ void __launch_bounds__(VT1) verify_sum_kernel(VerifyKArgs a, VPlan P)
   }
 }
 
-// Row j of batch entry b from the slice summaries: the max, and the proven
-// interval of the fixed-point normaliser.
-__device__ void vrow_bounds_of(const VRowSum* rs, int G1, float Tc, int V, float* m_out, uint64_t* zlo,
-                               uint64_t* zhi) {
-  float m = -INFINITY;
-  for (int s = 0; s < G1; ++s) m = fmaxf(m, rs[s].m);
+// Row j's max and the proven interval of its fixed-point normaliser, from
+// its slice summaries.  Every lane of a full wave calls it; lane l < G1
+// passes slice l's summary (valid), and every lane gets the results.
+__device__ __forceinline__ void vrow_bounds_w(const VRowSum& r, bool valid, float Tc, int V, float* m_out,
+                                              uint64_t* zlo, uint64_t* zhi) {
+  const float m = wmax_f(valid ? r.m : -INFINITY);
   // the float rescale's relative error (a few ulp) is far inside VEPS
-  double zf = 0.0;
-  if (m != -INFINITY)
-    for (int s = 0; s < G1; ++s)
-      if (rs[s].m != -INFINITY) zf += rs[s].zf * (double)__expf((rs[s].m - m) / Tc);
+  const double t = (valid && m != -INFINITY && r.m != -INFINITY) ? r.zf * (double)__expf((r.m - m) / Tc) : 0.0;
+  const double zf = wsum_f64(t);
   const double SC = 17592186044416.0, LIM = 4.0e18;
   const double lo = zf * SC * (1.0 - VEPS) - (double)V, hi = zf * SC * (1.0 + VEPS) + (double)V;
   *m_out = m;
@@ -368,91 +411,98 @@ __device__ void vrow_bounds_of(const VRowSum* rs, int G1, float Tc, int V, float
   *zhi = m == -INFINITY ? 0ull : (hi >= LIM ? (1ull << 62) : (uint64_t)ceil(hi));
 }
 
-// Wave-level reads (every lane of a full wave calls them): lane s reads one
-// row summary or one partial sum, so the reads are a single round trip, and
-// DPP reductions finish them; every lane gets the result.
-//  * row j's max from its G1 <= 8 slice summaries;
-//  * the sum of cnt <= 64 per-slice partial sums.
-__device__ __forceinline__ float vrow_max_w(const VerifyKArgs& a, const VPlan& P, int b, int j) {
-  const int lane = threadIdx.x & 63;
-  const VRowSum* rs = P.summ + ((long long)b * (a.n + 1) + j) * P.G1;
-  return wmax_f(lane < P.G1 ? rs[lane].m : -INFINITY);
-}
+// The sum of cnt <= 64 per-slice partial sums: lane s reads one, so the
+// reads are a single round trip, and a DPP reduction finishes them; every
+// lane of the (full) wave gets the result.
 __device__ __forceinline__ uint64_t vparts_sum_w(const unsigned long long* p, int cnt) {
   const int lane = threadIdx.x & 63;
   return wsum_u64(lane < cnt ? (uint64_t)p[lane] : 0ull);
 }
 
 __global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P) {
+  constexpr int NWV = VT2 / 64;              // waves
+  constexpr int RPW = (64 + NWV - 1) / NWV;  // rows j <= n < 64 per wave
   __shared__ VSmem sm;
   __shared__ int s_state[64];
   __shared__ float s_m[64];
-  __shared__ VRowSum s_rs[64 * 8];  // rows j < n (n < 64), G1 <= 8 summaries each
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int b = blockIdx.x / P.G2, s = blockIdx.x - b * P.G2;
   const int n = a.n, V = a.V, G1 = P.G1;
-  // Every summary of rows j < n in one round trip, staged in LDS (rows of
-  // one batch entry are contiguous), with each row's draft token and uniform
-  // read alongside.
-  for (int k = tid; k < n * G1; k += VT2) s_rs[k] = P.summ[(long long)b * (n + 1) * G1 + k];
-  int tk = 0;
+  // One round trip: wave w reads the slice summaries of rows j = w + NWV q
+  // (lane l: slice l), and its lane q the draft token, uniform and token
+  // record of row w + NWV q.
+  VRowSum r[RPW];
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    const int j = w + NWV * q;
+    r[q].m = -INFINITY;
+    r[q].zf = 0.0;
+    if (j <= n && lane < G1) r[q] = P.summ[((long long)b * (n + 1) + j) * G1 + lane];
+  }
+  const int jl = w + NWV * lane;
+  int tk = -1;
   float u = 0.0f;
-  if (tid < n) {
-    tk = a.tok[(long long)b * n + tid];
-    u = a.u[(long long)b * (n + 1) + tid];
+  VTokRec tr;
+  tr.xt = 0.0f;
+  tr.q = 0.0f;
+  if (lane < RPW && jl < n) {
+    tk = a.tok[(long long)b * n + jl];
+    u = a.u[(long long)b * (n + 1) + jl];
+    tr = P.trec[(long long)b * n + jl];
+  }
+  // every row's max and bounds (wave-wide), and for rows j < n the accept
+  // test by lane q: 0 accept, 1 reject, 2 undecided by the bounds
+#pragma unroll
+  for (int q = 0; q < RPW; ++q) {
+    const int j = w + NWV * q;
+    if (j <= n) {
+      float m;
+      uint64_t zlo, zhi;
+      vrow_bounds_w(r[q], lane < G1, a.Tc, V, &m, &zlo, &zhi);
+      if (lane == q) {
+        s_m[j] = m;
+        if (j < n) {
+          int st;
+          if (tk < 0 || tk >= V) {
+            st = 1;
+          } else {
+            const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(tr.xt, m, a.Tc));
+            if (reject_fused(u, tr.q, zlo, W)) st = 1;
+            else if (!reject_fused(u, tr.q, zhi, W)) st = 0;
+            else st = 2;
+          }
+          s_state[j] = st;
+        }
+      }
+    }
   }
   __syncthreads();
-  // decisions: 0 accept, 1 reject, 2 undecided by the bounds
-  if (tid < n) {
-    const int j = tid;
-    float m;
-    uint64_t zlo, zhi;
-    vrow_bounds_of(s_rs + j * G1, G1, a.Tc, V, &m, &zlo, &zhi);
-    s_m[j] = m;
-    int st;
-    if (tk < 0 || tk >= V) {
-      st = 1;
-    } else {
-      const float xt = a.target[((long long)b * (n + 1) + j) * V + tk];
-      const float q = a.draft[((long long)b * n + j) * V + tk];
-      const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(xt, m, a.Tc));
-      if (reject_fused(u, q, zlo, W)) st = 1;
-      else if (!reject_fused(u, q, zhi, W)) st = 0;
-      else st = 2;
-    }
-    s_state[j] = st;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int j = 0, und = 0;
-    for (; j < n; ++j) {
-      if (s_state[j] == 0) continue;
-      if (s_state[j] == 2) und = 1;
-      break;
-    }
-    if (P.force_exact) und = 1;
-    sm.bcasti[0] = j;
-    sm.bcasti[1] = und;
-    if (s == 0) {
-      P.jst[2 * b] = j;
-      P.jst[2 * b + 1] = und;
+  // j*, the first position not accepted (n when all are)
+  if (w == 0) {
+    const int st = lane < n ? s_state[lane] : 0;
+    const unsigned long long nz = __ballot(st != 0);
+    const int j = nz ? (int)__ffsll((long long)nz) - 1 : n;
+    const int und = ((nz && s_state[j] == 2) || P.force_exact) ? 1 : 0;
+    if (lane == 0) {
+      sm.bcasti[0] = j;
+      sm.bcasti[1] = und;
+      if (s == 0) *(int4*)(P.jst + 4 * b) = make_int4(j, und, __float_as_int(s_m[j]), 0);
     }
   }
   __syncthreads();
   const int js = sm.bcasti[0];
   if (sm.bcasti[1]) return;
+  const float m = s_m[js];
   const float* x = a.target + ((long long)b * (n + 1) + js) * V;
   const int v0 = s * P.SL2, v1 = min(V, v0 + P.SL2);
-  // the slice (at most 2 float4 per thread: SL2 <= 8192) is read before the
-  // row max is needed; positions past the slice (the slice may be empty) read
-  // the row's first float4 and are ignored
+  // the slice (at most 2 float4 per thread: SL2 <= 8192); positions past the
+  // slice (the slice may be empty) read the row's first float4 and are ignored
   float4 c[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int i = v0 + (tid + k * VT2) * 4;
     c[k] = *(const float4*)(x + (i < v1 ? i : 0));
   }
-  const float m = js < n ? s_m[js] : vrow_max_w(a, P, b, js);
   uint64_t z = 0;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -471,14 +521,16 @@ __global__ void __launch_bounds__(VT2) verify_resid_kernel(VerifyKArgs a, VPlan 
   const int tid = threadIdx.x;
   const int b = blockIdx.x / P.G2, s = blockIdx.x - b * P.G2;
   const int n = a.n, V = a.V;
-  const int js = P.jst[2 * b];
-  if (P.jst[2 * b + 1] || js >= n) return;
+  const int4 jr = *(const int4*)(P.jst + 4 * b);
+  const int js = jr.x;
+  if (jr.y || js >= n) return;
+  const float m = __int_as_float(jr.z);
   const float* x = a.target + ((long long)b * (n + 1) + js) * V;
   const float* q = a.draft + ((long long)b * n + js) * V;
   const int v0 = s * P.SL2, v1 = min(V, v0 + P.SL2);
-  // the slice (at most 2 float4 of each row per thread), the partial sums
-  // and the summaries are all read in one round trip; positions past the
-  // slice read the row's first float4 and are ignored
+  // the slice (at most 2 float4 of each row per thread) and the partial sums
+  // are read in one round trip; positions past the slice read the row's
+  // first float4 and are ignored
   float4 c[2], d[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -487,7 +539,6 @@ __global__ void __launch_bounds__(VT2) verify_resid_kernel(VerifyKArgs a, VPlan 
     d[k] = *(const float4*)(q + ic);
   }
   const uint64_t Z = vparts_sum_w(P.zpart + (long long)b * P.G2, P.G2);
-  const float m = vrow_max_w(a, P, b, js);
   uint64_t r = 0;
   auto res = [&](float xv, float qv) {
     const uint64_t w = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(xv, m, a.Tc));
@@ -606,19 +657,22 @@ __global__ void __launch_bounds__(1024) verify_pick_kernel(VerifyKArgs a, VPlan 
   __shared__ VSmem sm;
   const int b = blockIdx.x, tid = threadIdx.x;
   const int n = a.n, V = a.V;
-  const int js = P.jst[2 * b];
-  if (P.jst[2 * b + 1]) {
+  // j*, its row max and lane t's partial sums of slice t in one round trip
+  // (the residual sums exist only when j* < n); DPP sums and a scan over the
+  // lanes pick the slice
+  const int lane = tid & 63;
+  const bool ls = lane < P.G2;
+  const int4 jr = *(const int4*)(P.jst + 4 * b);
+  const uint64_t zp = ls ? (uint64_t)P.zpart[(long long)b * P.G2 + lane] : 0ull;
+  const uint64_t rraw = ls ? (uint64_t)P.rpart[(long long)b * P.G2 + lane] : 0ull;
+  const float ub = a.u[(long long)b * (n + 1) + n];
+  if (jr.y) {
     verify_exact_entry(a, b, sm);
     return;
   }
-  // lane t holds slice t's partial sums (one round trip); DPP sums and a
-  // scan over the lanes pick the slice
-  const int lane = tid & 63;
-  const bool ls = lane < P.G2;
-  const uint64_t zp = ls ? (uint64_t)P.zpart[(long long)b * P.G2 + lane] : 0ull;
-  const uint64_t rp = (ls && js < n) ? (uint64_t)P.rpart[(long long)b * P.G2 + lane] : 0ull;
-  const float ub = a.u[(long long)b * (n + 1) + n];
-  const float m = vrow_max_w(a, P, b, js);
+  const int js = jr.x;
+  const float m = __int_as_float(jr.z);
+  const uint64_t rp = js < n ? rraw : 0ull;
   const uint64_t Z = wsum_u64(zp), R = wsum_u64(rp);
   // residual mass when rejected and positive, else the row's own weights
   const bool use_r = js < n && R > 0;
@@ -653,14 +707,18 @@ __global__ void __launch_bounds__(1024) verify_pick_kernel(VerifyKArgs a, VPlan 
 
 struct VHostPlan {
   int G1, SL1, G2, SL2;
-  size_t summ, jst, zpart, rpart, total;
+  size_t summ, trec, jst, zpart, rpart, total;
 };
 
 // Workspace: the per-position slots of the one-workgroup-per-row form, then
 // the sliced form's row summaries and per-entry sums.
 static VHostPlan vplan(int B, int n, int V) {
   VHostPlan h;
-  h.G1 = std::max(1, (V + VE1 - 1) / VE1);
+  // enough pass-1 slices to fill the chip (at least 1024 ids each), and at
+  // least enough that each fits one workgroup's loads
+  const int rows = std::max(1, std::max(B, 0) * (std::max(n, 0) + 1));
+  const int g_fill = std::min({VG1MAX, (VBLK1 + rows - 1) / rows, (V + 4 * VT1 - 1) / (4 * VT1)});
+  h.G1 = std::max({1, (V + VE1 - 1) / VE1, g_fill});
   h.SL1 = ((V + h.G1 - 1) / h.G1 + 3) / 4 * 4;
   h.G2 = std::max(1, std::min(VG2MAX, (256 + std::max(B, 1) - 1) / std::max(B, 1)));
   // a slice of the selected row must fit the final draw's register segments
@@ -670,8 +728,11 @@ static VHostPlan vplan(int B, int n, int V) {
   size_t off = (slots * 16 + 255) / 256 * 256;
   h.summ = off;
   off += (size_t)std::max(B, 0) * (std::max(n, 0) + 1) * h.G1 * sizeof(VRowSum);
+  h.trec = off;
+  off += (size_t)std::max(B, 0) * std::max(n, 0) * sizeof(VTokRec);
+  off = (off + 15) / 16 * 16;
   h.jst = off;
-  off += (size_t)std::max(B, 0) * 8;
+  off += (size_t)std::max(B, 0) * 16;
   off = (off + 15) / 16 * 16;
   h.zpart = off;
   off += (size_t)std::max(B, 0) * h.G2 * 8;
@@ -692,6 +753,7 @@ static int launch_verify_sliced(const VerifyKArgs& k, const VHostPlan& h, char* 
   P.G2 = h.G2;
   P.SL2 = h.SL2;
   P.summ = (VRowSum*)(ws + h.summ);
+  P.trec = (VTokRec*)(ws + h.trec);
   P.jst = (int32_t*)(ws + h.jst);
   P.zpart = (unsigned long long*)(ws + h.zpart);
   P.rpart = (unsigned long long*)(ws + h.rpart);
@@ -773,10 +835,12 @@ extern "C" int wh_verify_fused(const wh_verify_args* args, void* stream) {
   size_t slots = (size_t)args->B * args->n;
   char* ws = (char*)args->workspace;
   hipStream_t st0 = (hipStream_t)stream;
-  // the sliced passes need 16-byte aligned rows (float4 loads) and n < 64
+  // the sliced passes need 16-byte aligned rows (float4 loads) and
+  // workspace (16-byte records), and n < 64
   const VHostPlan vh = vplan(args->B, args->n, args->V);
   const bool sliced = args->temperature > 0.0f && args->n > 0 && args->n < 64 && args->V % 4 == 0 &&
-                      (uintptr_t)args->target % 16 == 0 && (uintptr_t)args->draft % 16 == 0 && ws;
+                      (uintptr_t)args->target % 16 == 0 && (uintptr_t)args->draft % 16 == 0 && ws &&
+                      (uintptr_t)ws % 16 == 0;
   if (sliced) return launch_verify_sliced(k, vh, ws, st0);
   k.rz = (unsigned long long*)ws;
   k.rmax = (float*)(ws + slots * 8);
