@@ -53,6 +53,14 @@ __device__ __forceinline__ uint4 load_stream16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// d / t in float32, correctly rounded, from r = 1.0 / (double)t (rounded to
+// double): the double product is within 2^-52 (relative) of d / t, while a
+// quotient of two 24-bit significands is never a midpoint between floats and
+// lies at least about 2^-49 (relative) from every one, so the product rounds
+// to the same float -- a multiply in place of the division sequence.  The
+// same holds for zeros, infinities, NaNs and subnormal results.
+__device__ __forceinline__ float div_by_recip(float d, double r) { return (float)((double)d * r); }
+
 // float32 mantissa/exponent split: x = M * 2^(e - 24), M a 24-bit integer.
 __device__ __forceinline__ uint64_t mant24(float x, int* e) {
   float fr = frexpf(x, e);

@@ -1287,7 +1287,7 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
 
   // Draw: integer inverse CDF in vocabulary order over the kept slots.
   const float invT = (float)(1.0 / (double)rp.T);
-  const float Tc = (float)fmax((double)rp.T, 1e-5);
+  const double rTc = 1.0 / (double)(float)fmax((double)rp.T, 1e-5);
   uint64_t ZV;
   int tok = 0;
   if (all_kept) {
@@ -1325,7 +1325,7 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
     for (int t = 0; t < NS; ++t)
       if (st.on(t))
         out[st.ci[t]] = a.out_mode == WH_OUT_MASKED ? st.cl[t]
-                                                    : (float)((double)chain_scale(a.chain, st.cl[t] - m, invT, Tc) - lz);
+                                                    : (float)((double)chain_scale(a.chain, st.cl[t] - m, invT, rTc) - lz);
   }
   return 0;
 }
@@ -1365,10 +1365,10 @@ __device__ __noinline__ int merge_block(const SampleKArgs* ap, const FastPlan* p
   const ZBounds zb = z_bounds_loop(hd, G, m, Scand);
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
   const float invT = (float)(1.0 / (double)rp.T);
-  const float Tc = (float)fmax((double)rp.T, 1e-5);
+  const double rTc = 1.0 / (double)(float)fmax((double)rp.T, 1e-5);
   const Pred pr = st.pr;
   const CandSource src = st.src;
-  auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, Tc)); };
+  auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, rTc)); };
   uint64_t zv = 0;
   int nk = 0;
   src.each([&](int i, float l) {
@@ -1408,7 +1408,7 @@ __device__ __noinline__ int merge_block(const SampleKArgs* ap, const FastPlan* p
     const double lz = log(ldexp((double)ZV, -44));
     src.each([&](int i, float l) {
       if (!pr.keep(i, l)) return;
-      out[i] = a.out_mode == WH_OUT_MASKED ? l : (float)((double)chain_scale(a.chain, l - m, invT, Tc) - lz);
+      out[i] = a.out_mode == WH_OUT_MASKED ? l : (float)((double)chain_scale(a.chain, l - m, invT, rTc) - lz);
     });
   }
   return 4;
@@ -1489,7 +1489,7 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
     const float thr = split ? m + min_p_log(a, rp.min_p) : -INFINITY;
     const bool tscale = rp.T != 1.0f;
     const float invT = (float)(1.0 / (double)rp.T);
-    const float Tc = (float)fmax((double)rp.T, 1e-5);
+    const double rTc = 1.0 / (double)(float)fmax((double)rp.T, 1e-5);
     const int hn = lane < G ? hd.n : 0;
     uint64_t mv[3] = {0ull, 0ull, 0ull};  // hot mass, covered hot mass, cold mass
     uint64_t e[QW], bh[QW];
@@ -1528,7 +1528,7 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
         const int i = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bh[j] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bh[j], 0u));
         uint64_t dw = e[j];
         if (tscale) {
-          dw = exp_fix44(chain_scale(a.chain, __int_as_float(spec[j].x) - m, invT, Tc));
+          dw = exp_fix44(chain_scale(a.chain, __int_as_float(spec[j].x) - m, invT, rTc));
           hl.dw[i] = dw;
         }
         hl.cand[i] = spec[j];

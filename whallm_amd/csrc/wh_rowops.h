@@ -237,8 +237,8 @@ __device__ uint64_t radix_select(const Src& src, const Pred& pr, Meas meas, uint
   return prefix;
 }
 
-__device__ __forceinline__ float chain_scale(int chain, float d, float invT, float Tc) {
-  return chain == WH_CHAIN_MLX ? d * invT : d / Tc;
+__device__ __forceinline__ float chain_scale(int chain, float d, float invT, double rTc) {
+  return chain == WH_CHAIN_MLX ? d * invT : div_by_recip(d, rTc);
 }
 
 // The whole exact algorithm for row b by one workgroup (64..1024 threads, a
@@ -347,7 +347,7 @@ __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_sm
 
   // Draw: per-thread contiguous segments, integer inverse CDF in vocab order.
   const float invT = (float)(1.0 / (double)T);
-  const float Tc = (float)fmax((double)T, 1e-5);
+  const double rTc = 1.0 / (double)(float)fmax((double)T, 1e-5);
   const int seg = (V + nt - 1) / nt;
   const int lo = min(V, tid * seg), hi = min(V, lo + seg);
   uint64_t s = 0;
@@ -356,7 +356,7 @@ __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_sm
     float l = rc.val(i);
     if (!pr.keep(i, l)) continue;
     ++cnt;
-    s += exp_fix44(chain_scale(a.chain, l - m, invT, Tc));
+    s += exp_fix44(chain_scale(a.chain, l - m, invT, rTc));
   }
   uint64_t ZV;
   uint64_t excl = block_exclusive_scan_u64(s, sm.scratch64, &ZV);
@@ -370,7 +370,7 @@ __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_sm
       for (int i = lo; i < hi; ++i) {
         float l = rc.val(i);
         if (!pr.keep(i, l)) continue;
-        c += exp_fix44(chain_scale(a.chain, l - m, invT, Tc));
+        c += exp_fix44(chain_scale(a.chain, l - m, invT, rTc));
         if (c > tgt) { a.tokens[b] = i; break; }
       }
     }
@@ -385,7 +385,7 @@ __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_sm
     const double lz = log(ldexp((double)ZV, -44));
     for (int i = tid; i < V; i += nt) {
       float l = rc.val(i);
-      out[i] = pr.keep(i, l) ? (float)((double)chain_scale(a.chain, l - m, invT, Tc) - lz) : -INFINITY;
+      out[i] = pr.keep(i, l) ? (float)((double)chain_scale(a.chain, l - m, invT, rTc) - lz) : -INFINITY;
     }
   }
 }

@@ -27,6 +27,7 @@ struct VerifyKArgs {
   int B, n, V;
   float T;     // temperature
   float Tc;    // fl32(max(T, 1e-5))
+  double rTc;  // 1 / (double)Tc: divisions by Tc as exact multiplies
   const float* target;
   const float* draft;
   const int32_t* tok;
@@ -207,14 +208,14 @@ __global__ void __launch_bounds__(1024) verify_fused_rows_kernel(VerifyKArgs a) 
   const float m = block_max(x, V, sm);
   uint64_t z = 0;
   if (m != -INFINITY)
-    for (int i = tid; i < V; i += blockDim.x) z += exp_fix44((x[i] - m) / a.Tc);
+    for (int i = tid; i < V; i += blockDim.x) z += exp_fix44(div_by_recip(x[i] - m, a.rTc));
   const uint64_t Z = block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
   if (tid == 0) {
     bool rj;
     if (tk < 0 || tk >= V) {
       rj = true;
     } else {
-      uint64_t W = m == -INFINITY ? 0 : exp_fix44((x[tk] - m) / a.Tc);
+      uint64_t W = m == -INFINITY ? 0 : exp_fix44(div_by_recip(x[tk] - m, a.rTc));
       float q = a.draft[slot * V + tk];
       rj = reject_fused(a.u[(long long)b * (a.n + 1) + j], q, Z, W);
     }
@@ -247,10 +248,10 @@ __global__ void __launch_bounds__(1024) verify_fused_draw_kernel(VerifyKArgs a) 
     m = block_max(x, V, sm);
     uint64_t z = 0;
     if (m != -INFINITY)
-      for (int i = tid; i < V; i += blockDim.x) z += exp_fix44((x[i] - m) / a.Tc);
+      for (int i = tid; i < V; i += blockDim.x) z += exp_fix44(div_by_recip(x[i] - m, a.rTc));
     Z = block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
   }
-  auto wt = [&](int i) { return m == -INFINITY ? (uint64_t)0 : exp_fix44((x[i] - m) / a.Tc); };
+  auto wt = [&](int i) { return m == -INFINITY ? (uint64_t)0 : exp_fix44(div_by_recip(x[i] - m, a.rTc)); };
   int tok = 0;
   uint64_t tot;
   if (j == n) {
@@ -324,7 +325,8 @@ struct VPlan {
   unsigned long long* rpart;  // [B, G2] residual mass of row j*
 };
 
-__device__ __forceinline__ float vweight_arg(float x, float m, float Tc) { return (x - m) / Tc; }
+// (x - m) / Tc, exactly as the division rounds (rTc = 1 / (double)Tc)
+__device__ __forceinline__ float vweight_arg(float x, float m, double rTc) { return div_by_recip(x - m, rTc); }
 
 __global__ void __launch_bounds__(VT1) verify_sum_kernel(VerifyKArgs a, VPlan P) {
   __shared__ float s_m[VT1 / 64];
@@ -466,7 +468,7 @@ __global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P
           if (tk < 0 || tk >= V) {
             st = 1;
           } else {
-            const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(tr.xt, m, a.Tc));
+            const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(tr.xt, m, a.rTc));
             if (reject_fused(u, tr.q, zlo, W)) st = 1;
             else if (!reject_fused(u, tr.q, zhi, W)) st = 0;
             else st = 2;
@@ -508,8 +510,8 @@ __global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P
   for (int k = 0; k < 2; ++k) {
     const int i = v0 + (tid + k * VT2) * 4;
     if (m != -INFINITY && i < v1) {
-      z += exp_fix44(vweight_arg(c[k].x, m, a.Tc)) + exp_fix44(vweight_arg(c[k].y, m, a.Tc));
-      z += exp_fix44(vweight_arg(c[k].z, m, a.Tc)) + exp_fix44(vweight_arg(c[k].w, m, a.Tc));
+      z += exp_fix44(vweight_arg(c[k].x, m, a.rTc)) + exp_fix44(vweight_arg(c[k].y, m, a.rTc));
+      z += exp_fix44(vweight_arg(c[k].z, m, a.rTc)) + exp_fix44(vweight_arg(c[k].w, m, a.rTc));
     }
   }
   const uint64_t zt = block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
@@ -541,7 +543,7 @@ __global__ void __launch_bounds__(VT2) verify_resid_kernel(VerifyKArgs a, VPlan 
   const uint64_t Z = vparts_sum_w(P.zpart + (long long)b * P.G2, P.G2);
   uint64_t r = 0;
   auto res = [&](float xv, float qv) {
-    const uint64_t w = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(xv, m, a.Tc));
+    const uint64_t w = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(xv, m, a.rTc));
     const uint64_t qz = floor_qz(qv, Z);
     return w > qz ? w - qz : (uint64_t)0;
   };
@@ -617,7 +619,7 @@ __device__ void verify_exact_entry(const VerifyKArgs& a, int b, VSmem& sm) {
     m = block_max(x, V, sm);
     uint64_t z = 0;
     if (m != -INFINITY)
-      for (int i = tid; i < V; i += blockDim.x) z += exp_fix44(vweight_arg(x[i], m, a.Tc));
+      for (int i = tid; i < V; i += blockDim.x) z += exp_fix44(vweight_arg(x[i], m, a.rTc));
     Z = block_reduce(z, sm.scratch64, OpSumU64(), (uint64_t)0);
     if (j == n) break;
     const int tk = a.tok[(long long)b * n + j];
@@ -625,14 +627,14 @@ __device__ void verify_exact_entry(const VerifyKArgs& a, int b, VSmem& sm) {
     if (tk < 0 || tk >= V) {
       rj = true;
     } else {
-      const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(x[tk], m, a.Tc));
+      const uint64_t W = m == -INFINITY ? 0ull : exp_fix44(vweight_arg(x[tk], m, a.rTc));
       rj = reject_fused(a.u[(long long)b * (n + 1) + j], a.draft[((long long)b * n + j) * V + tk], Z, W);
     }
     if (rj) break;
   }
   const float* x = a.target + ((long long)b * (n + 1) + j) * V;
   const float u = a.u[(long long)b * (n + 1) + n];
-  auto wt = [&](int i) { return m == -INFINITY ? (uint64_t)0 : exp_fix44(vweight_arg(x[i], m, a.Tc)); };
+  auto wt = [&](int i) { return m == -INFINITY ? (uint64_t)0 : exp_fix44(vweight_arg(x[i], m, a.rTc)); };
   int tok = 0;
   uint64_t tot;
   if (j == n) {
@@ -688,7 +690,7 @@ __global__ void __launch_bounds__(1024) verify_pick_kernel(VerifyKArgs a, VPlan 
     const uint64_t rem = tgt - (lane_u64(incl, ss) - lane_u64(part, ss));
     const float* x = a.target + ((long long)b * (n + 1) + js) * V;
     const int v0 = ss * P.SL2, v1 = min(V, v0 + P.SL2);
-    auto wt = [&](float xv) { return m == -INFINITY ? (uint64_t)0 : exp_fix44(vweight_arg(xv, m, a.Tc)); };
+    auto wt = [&](float xv) { return m == -INFINITY ? (uint64_t)0 : exp_fix44(vweight_arg(xv, m, a.rTc)); };
     if (use_r) {
       const float* q = a.draft + ((long long)b * n + js) * V;
       tok = segment_find<VSEG4>(v0, v1, rem, x, q, [&](float xv, float qv) {
@@ -793,6 +795,7 @@ static VerifyKArgs to_kargs(const wh_verify_args* p) {
   k.V = p->V;
   k.T = p->temperature;
   k.Tc = (float)std::fmax((double)p->temperature, 1e-5);
+  k.rTc = 1.0 / (double)k.Tc;
   k.target = p->target;
   k.draft = p->draft;
   k.tok = p->draft_tokens;
