@@ -277,7 +277,8 @@ __global__ void __launch_bounds__(1024) verify_fused_draw_kernel(VerifyKArgs a) 
 //      One HBM pass over the target rows.  The first slice's workgroup also
 //      records the target logit and draft probability at the row's draft
 //      token.
-//   2. verify_prep_kernel, G2 workgroups per batch entry: each recomputes the
+//   2. verify_prep_kernel, G2 workgroups per batch entry (slices of at most
+//      4096 ids, about four workgroups per CU): each recomputes the
 //      accept / reject decisions from the row summaries -- the normaliser Z
 //      lies in [Zlo, Zhi] from the float sums, and u q Z > W is decided from
 //      both ends (W exact, from the draft token's logit); the first
@@ -295,13 +296,16 @@ constexpr int VL1 = 8;         // float4 loads per thread, pass 1
 constexpr int VE1 = 4 * VL1 * VT1;  // elements per pass-1 slice, at most (8192)
 constexpr int VBLK1 = 2048;    // pass-1 workgroups aimed for (eight per CU)
 constexpr int VG1MAX = 64;     // pass-1 slices per row, at most (one wave lane each)
-constexpr int VT2 = 1024;      // threads, passes 2 and 3
-constexpr int VG2MAX = 16;     // slices of the selected row
-constexpr int VSEG4 = 2;       // float4 groups per thread in the final draw (1024 threads: 8192 ids)
+constexpr int VT2 = 256;       // threads, passes 2 and 3 (NQ float4 per thread, NQ = 2 or 4)
+constexpr int VT3 = 1024;      // threads, pass 4
+constexpr int VG2MAX = 64;     // slices of the selected row, at most (one wave lane each)
+constexpr int VSEG4 = 1;       // float4 groups per thread in the final draw
+constexpr int VE2 = 4 * VSEG4 * VT3;  // ids per slice of the selected row, at most (4096)
 constexpr double VEPS = 2e-4;  // relative slack of the float normaliser
-// slices of the selected row hold at most 4 * VSEG4 * VT2 ids: the prep and
-// residual passes read them as 2 float4 per thread
-static_assert(VSEG4 == 2 && VT2 == 1024, "sliced verify: 2 float4 per thread cover a slice");
+// a slice of the selected row fits the final draw's registers and the
+// prep / residual passes' loads (4 float4 per thread at most)
+static_assert(VE2 == 4 * 4 * VT2, "sliced verify: 4 float4 per thread cover a slice");
+static_assert((WH_MAX_VOCAB + VE2 - 1) / VE2 <= VG2MAX, "slices of the selected row fit one wave's lanes");
 static_assert((WH_MAX_VOCAB + VE1 - 1) / VE1 <= VG1MAX, "pass-1 slices of a row fit one wave's lanes");
 
 struct VRowSum {
@@ -421,6 +425,7 @@ __device__ __forceinline__ uint64_t vparts_sum_w(const unsigned long long* p, in
   return wsum_u64(lane < cnt ? (uint64_t)p[lane] : 0ull);
 }
 
+template <int NQ>
 __global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P) {
   constexpr int NWV = VT2 / 64;              // waves
   constexpr int RPW = (64 + NWV - 1) / NWV;  // rows j <= n < 64 per wave
@@ -497,17 +502,18 @@ __global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P
   const float m = s_m[js];
   const float* x = a.target + ((long long)b * (n + 1) + js) * V;
   const int v0 = s * P.SL2, v1 = min(V, v0 + P.SL2);
-  // the slice (at most 2 float4 per thread: SL2 <= 8192); positions past the
-  // slice (the slice may be empty) read the row's first float4 and are ignored
-  float4 c[2];
+  // the slice (at most NQ float4 per thread: SL2 <= 4 NQ VT2); positions
+  // past the slice (the slice may be empty) read the row's first float4 and
+  // are ignored
+  float4 c[NQ];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
+  for (int k = 0; k < NQ; ++k) {
     const int i = v0 + (tid + k * VT2) * 4;
     c[k] = *(const float4*)(x + (i < v1 ? i : 0));
   }
   uint64_t z = 0;
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
+  for (int k = 0; k < NQ; ++k) {
     const int i = v0 + (tid + k * VT2) * 4;
     if (m != -INFINITY && i < v1) {
       z += exp_fix44(vweight_arg(c[k].x, m, a.rTc)) + exp_fix44(vweight_arg(c[k].y, m, a.rTc));
@@ -518,6 +524,7 @@ __global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P
   if (tid == 0) P.zpart[(long long)b * P.G2 + s] = zt;
 }
 
+template <int NQ>
 __global__ void __launch_bounds__(VT2) verify_resid_kernel(VerifyKArgs a, VPlan P) {
   __shared__ VSmem sm;
   const int tid = threadIdx.x;
@@ -530,12 +537,12 @@ __global__ void __launch_bounds__(VT2) verify_resid_kernel(VerifyKArgs a, VPlan 
   const float* x = a.target + ((long long)b * (n + 1) + js) * V;
   const float* q = a.draft + ((long long)b * n + js) * V;
   const int v0 = s * P.SL2, v1 = min(V, v0 + P.SL2);
-  // the slice (at most 2 float4 of each row per thread) and the partial sums
-  // are read in one round trip; positions past the slice read the row's
+  // the slice (at most NQ float4 of each row per thread) and the partial
+  // sums are read in one round trip; positions past the slice read the row's
   // first float4 and are ignored
-  float4 c[2], d[2];
+  float4 c[NQ], d[NQ];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
+  for (int k = 0; k < NQ; ++k) {
     const int i = v0 + (tid + k * VT2) * 4, ic = i < v1 ? i : 0;
     c[k] = *(const float4*)(x + ic);
     d[k] = *(const float4*)(q + ic);
@@ -548,7 +555,7 @@ __global__ void __launch_bounds__(VT2) verify_resid_kernel(VerifyKArgs a, VPlan 
     return w > qz ? w - qz : (uint64_t)0;
   };
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
+  for (int k = 0; k < NQ; ++k) {
     const int i = v0 + (tid + k * VT2) * 4;
     if (i < v1) r += res(c[k].x, d[k].x) + res(c[k].y, d[k].y) + res(c[k].z, d[k].z) + res(c[k].w, d[k].w);
   }
@@ -655,7 +662,7 @@ __device__ void verify_exact_entry(const VerifyKArgs& a, int b, VSmem& sm) {
   }
 }
 
-__global__ void __launch_bounds__(1024) verify_pick_kernel(VerifyKArgs a, VPlan P) {
+__global__ void __launch_bounds__(VT3) verify_pick_kernel(VerifyKArgs a, VPlan P) {
   __shared__ VSmem sm;
   const int b = blockIdx.x, tid = threadIdx.x;
   const int n = a.n, V = a.V;
@@ -722,9 +729,12 @@ static VHostPlan vplan(int B, int n, int V) {
   const int g_fill = std::min({VG1MAX, (VBLK1 + rows - 1) / rows, (V + 4 * VT1 - 1) / (4 * VT1)});
   h.G1 = std::max({1, (V + VE1 - 1) / VE1, g_fill});
   h.SL1 = ((V + h.G1 - 1) / h.G1 + 3) / 4 * 4;
-  h.G2 = std::max(1, std::min(VG2MAX, (256 + std::max(B, 1) - 1) / std::max(B, 1)));
-  // a slice of the selected row must fit the final draw's register segments
-  h.G2 = std::max(h.G2, (V + 4 * VSEG4 * 1024 - 1) / (4 * VSEG4 * 1024));
+  // slices of the selected row: about 1024 prep / residual workgroups (four
+  // per CU) and small slices for the one-workgroup final draw, at least 1024
+  // ids each; a slice must fit the final draw's register segments
+  const int Bp = std::max(B, 1);
+  h.G2 = std::max(1, std::min({VG2MAX, (1024 + Bp - 1) / Bp, (V + 1023) / 1024}));
+  h.G2 = std::max(h.G2, (V + VE2 - 1) / VE2);
   h.SL2 = ((V + h.G2 - 1) / h.G2 + 3) / 4 * 4;
   const size_t slots = (size_t)std::max(B, 0) * (size_t)std::max(n, 0);
   size_t off = (slots * 16 + 255) / 256 * 256;
@@ -762,13 +772,17 @@ static int launch_verify_sliced(const VerifyKArgs& k, const VHostPlan& h, char* 
   hipLaunchKernelGGL(verify_sum_kernel, dim3(k.B * (k.n + 1) * h.G1), dim3(VT1), 0, st, k, P);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "verify_sum_kernel launch failed: %s", hipGetErrorString(e));
-  hipLaunchKernelGGL(verify_prep_kernel, dim3(k.B * h.G2), dim3(VT2), 0, st, k, P);
+  // float4 loads per thread in the prep and residual passes
+  const bool nq2 = h.SL2 <= 2 * 4 * VT2;
+  if (nq2) hipLaunchKernelGGL(verify_prep_kernel<2>, dim3(k.B * h.G2), dim3(VT2), 0, st, k, P);
+  else hipLaunchKernelGGL(verify_prep_kernel<4>, dim3(k.B * h.G2), dim3(VT2), 0, st, k, P);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "verify_prep_kernel launch failed: %s", hipGetErrorString(e));
-  hipLaunchKernelGGL(verify_resid_kernel, dim3(k.B * h.G2), dim3(VT2), 0, st, k, P);
+  if (nq2) hipLaunchKernelGGL(verify_resid_kernel<2>, dim3(k.B * h.G2), dim3(VT2), 0, st, k, P);
+  else hipLaunchKernelGGL(verify_resid_kernel<4>, dim3(k.B * h.G2), dim3(VT2), 0, st, k, P);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "verify_resid_kernel launch failed: %s", hipGetErrorString(e));
-  hipLaunchKernelGGL(verify_pick_kernel, dim3(k.B), dim3(1024), 0, st, k, P);
+  hipLaunchKernelGGL(verify_pick_kernel, dim3(k.B), dim3(VT3), 0, st, k, P);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "verify_pick_kernel launch failed: %s", hipGetErrorString(e));
   return WH_OK;
