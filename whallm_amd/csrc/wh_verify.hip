@@ -57,9 +57,22 @@ __device__ __forceinline__ bool reject_lp(float u, float g, float d) {
   return (double)u * 17592186044416.0 > (double)R;
 }
 
-// floor(q Z) for q clamped to [0, 1] (so the result is at most Z): the same
-// two 64-bit products as floor_theta_z.
-__device__ __forceinline__ uint64_t floor_qz(float q, uint64_t Z) { return floor_theta_z(q, Z); }
+// floor(q Z) for q clamped to [0, 1] (NaN and q <= 0 give 0), Z < 2^62, from
+// q's bits: q <= 0, NaN or q < 2^-62 (then q Z < 1) give 0, q >= 1 gives Z;
+// otherwise q = M 2^-s with the 24-bit significand M and s = 150 - E in
+// [23, 85], and M Z = hi 2^32 + lo is shifted in two 64-bit pieces as in
+// floor_theta_z.  Equal to floor_theta_z(q, Z) for every float q.
+__device__ __forceinline__ uint64_t floor_qz(float q, uint64_t Z) {
+  const uint32_t b = __float_as_uint(q);
+  if ((int32_t)b <= 0 || b > 0x7F800000u) return 0;
+  if (b >= 0x3F800000u) return Z;
+  const int E = (int)(b >> 23);  // biased exponent, 1..126 here
+  if (E < 65) return 0;
+  const uint64_t M = (b & 0x7FFFFFu) | 0x800000u;
+  const int s = 150 - E;  // 24..85: both shifts below stay in [0, 53]
+  const uint64_t lo = M * (Z & 0xFFFFFFFFull), hi = M * (Z >> 32);
+  return s <= 32 ? (hi << (32 - s)) + (lo >> s) : (hi + (lo >> 32)) >> (s - 32);
+}
 
 // reject iff u * q * Z > W (exact)
 __device__ __forceinline__ bool reject_fused(float u, float q, uint64_t Z, uint64_t W) {
