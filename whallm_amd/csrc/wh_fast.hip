@@ -844,6 +844,8 @@ struct RegStore {
   uint64_t w[NS];  // exp_fix44(l - m) (replaced by the draw weights at the end)
   uint32_t al;
   uint64_t* bkt;  // 64 LDS buckets for the radix descents
+  uint64_t* lc;   // 64 LDS composites and 64 masses (lm) for the small top-p cut
+  uint64_t* lm;
   // masses of the alive set (all / covered) while no filter has changed it
   bool cached;
   uint64_t m_all, m_cov;
@@ -947,8 +949,38 @@ struct RegStore {
   // select the same element (order P).
   __device__ __forceinline__ bool keep_pcut(uint64_t Rlo, uint64_t Rhi, float tcov) {
     auto cov = [&](int t) { return cl[t] >= tcov; };
-    const uint64_t clo = select_desc<ORD_P, true>(cov, Rlo, bkt);
-    const uint64_t chi = select_desc<ORD_P, true>(cov, Rhi, bkt);
+    uint64_t clo, chi;
+    if (count_if(cov) <= 64) {
+      // At most one slot per lane (after a small top-k): the slots go to LDS,
+      // and each lane sums the masses of the composites at or above its own
+      // from broadcast reads.  Those inclusive sums grow in descending
+      // order, so the element where the sum first reaches R is the largest
+      // composite whose sum reaches R.
+      const int lane = threadIdx.x & 63;
+      int n = 0;
+#pragma unroll
+      for (int t = 0; t < NS; ++t) {
+        const bool p = on(t) && cov(t);
+        const uint64_t bal = __ballot(p);
+        if (p) {
+          const int i = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+          lc[i] = comp_p(fkey(cl[t]), ci[t]);
+          lm[i] = w[t];
+        }
+        n += (int)__popcll(bal);
+      }
+      wave_sync();
+      const uint64_t mine = lane < n ? lc[lane] : 0ull;
+      uint64_t incl = 0;
+      for (int j = 0; j < n; ++j) incl += lc[j] >= mine ? lm[j] : 0ull;
+      auto umax = [](uint64_t x, uint64_t y) { return x > y ? x : y; };
+      clo = dpp_reduce_u64(lane < n && incl >= Rlo ? mine : 0ull, umax);
+      chi = dpp_reduce_u64(lane < n && incl >= Rhi ? mine : 0ull, umax);
+      wave_sync();
+    } else {
+      clo = select_desc<ORD_P, true>(cov, Rlo, bkt);
+      chi = select_desc<ORD_P, true>(cov, Rhi, bkt);
+    }
     if (clo != chi) return false;
     keep_if([&](int t) { return comp_p(fkey(cl[t]), ci[t]) >= clo; });
     return true;
@@ -1264,6 +1296,9 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
   uint64_t wd[NS];
   st.al = 0;
   st.bkt = sm.bucket[0];
+  // the listing's per-lane sums are consumed by the totals before the filters
+  st.lc = sm.acc[0];
+  st.lm = sm.acc[1];
 #pragma unroll
   for (int t = 0; t < NS; ++t) {
     const bool valid = t * 64 + lane < N;
