@@ -844,8 +844,7 @@ struct RegStore {
   uint64_t w[NS];  // exp_fix44(l - m) (replaced by the draw weights at the end)
   uint32_t al;
   uint64_t* bkt;  // 64 LDS buckets for the radix descents
-  uint64_t* lc;   // 64 LDS composites and 64 masses (lm) for the small top-p cut
-  uint64_t* lm;
+  ulonglong2* lp;  // 64 LDS (composite, mass) pairs for the small top-p cut
   // masses of the alive set (all / covered) while no filter has changed it
   bool cached;
   uint64_t m_all, m_cov;
@@ -951,12 +950,14 @@ struct RegStore {
     auto cov = [&](int t) { return cl[t] >= tcov; };
     uint64_t clo, chi;
     if (count_if(cov) <= 64) {
-      // At most one slot per lane (after a small top-k): the slots go to LDS,
-      // and each lane sums the masses of the composites at or above its own
-      // from broadcast reads.  Those inclusive sums grow in descending
+      // At most one slot per lane (after a small top-k): the slots go to LDS
+      // as (composite, mass) pairs, zero-padded, and each lane sums the
+      // masses of the composites at or above its own from broadcast reads,
+      // eight pairs per step.  Those inclusive sums grow in descending
       // order, so the element where the sum first reaches R is the largest
       // composite whose sum reaches R.
       const int lane = threadIdx.x & 63;
+      lp[lane] = make_ulonglong2(0ull, 0ull);
       int n = 0;
 #pragma unroll
       for (int t = 0; t < NS; ++t) {
@@ -964,15 +965,20 @@ struct RegStore {
         const uint64_t bal = __ballot(p);
         if (p) {
           const int i = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-          lc[i] = comp_p(fkey(cl[t]), ci[t]);
-          lm[i] = w[t];
+          lp[i] = make_ulonglong2(comp_p(fkey(cl[t]), ci[t]), w[t]);
         }
         n += (int)__popcll(bal);
       }
       wave_sync();
-      const uint64_t mine = lane < n ? lc[lane] : 0ull;
+      const uint64_t mine = lane < n ? lp[lane].x : 0ull;
       uint64_t incl = 0;
-      for (int j = 0; j < n; ++j) incl += lc[j] >= mine ? lm[j] : 0ull;
+      for (int j0 = 0; j0 < n; j0 += 8) {  // j0 <= 56: every read is inside the 64 pairs
+        ulonglong2 e[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) e[q] = lp[j0 + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) incl += e[q].x >= mine ? e[q].y : 0ull;
+      }
       auto umax = [](uint64_t x, uint64_t y) { return x > y ? x : y; };
       clo = dpp_reduce_u64(lane < n && incl >= Rlo ? mine : 0ull, umax);
       chi = dpp_reduce_u64(lane < n && incl >= Rhi ? mine : 0ull, umax);
@@ -993,7 +999,7 @@ struct MergeSmem {
   // per lane, added by every listing wave: [0] hot mass, [1] hot mass at or
   // above tcov, [2] cold mass; [3] level-0 draw buckets (4096 ids each) over
   // every hot candidate
-  uint64_t acc[4][64];
+  alignas(16) uint64_t acc[4][64];
   ZParts zp;  // the summaries' share of the normaliser bounds
   int n;      // hot candidates listed
   int tok;    // wave 1's draw over the whole list
@@ -1297,8 +1303,7 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
   st.al = 0;
   st.bkt = sm.bucket[0];
   // the listing's per-lane sums are consumed by the totals before the filters
-  st.lc = sm.acc[0];
-  st.lm = sm.acc[1];
+  st.lp = (ulonglong2*)&sm.acc[0][0];
 #pragma unroll
   for (int t = 0; t < NS; ++t) {
     const bool valid = t * 64 + lane < N;
