@@ -333,7 +333,7 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
     for (; round < LADDER_ROUNDS && clo > target && hi != INFINITY; ++round) {
       const float span = hi - lo;
 #pragma unroll
-      for (int q = 0; q < RUNGS; ++q) x[q] = hi - span * (float)(q + 1) / (float)(RUNGS + 1);
+      for (int q = 0; q < RUNGS; ++q) x[q] = hi - span * ((float)(q + 1) / (float)(RUNGS + 1));  // a folded constant, no division
       ladder_count<R>(gm, patch, npatch, x, c, round, sm);
       bool f2 = false;
       float nlo = lo, nhi = hi;
@@ -369,7 +369,7 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
   if (nxt == sel) return sel;
   const float span = sel - nxt;
 #pragma unroll
-  for (int q = 0; q < RUNGS; ++q) x[q] = sel - span * (float)(q + 1) / (float)(RUNGS + 1);
+  for (int q = 0; q < RUNGS; ++q) x[q] = sel - span * ((float)(q + 1) / (float)(RUNGS + 1));
   ladder_count<R>(gm, patch, npatch, x, c, 1, sm);
   float best = sel;
 #pragma unroll
