@@ -913,23 +913,43 @@ struct RegStore {
     uint64_t prefix = cmax >> (6 * L);
     for (int lev = 0; lev < L; ++lev) {
       const int sh = 6 * (L - 1 - lev);
-      bucket[lane] = 0;
-      wave_sync();
+      uint64_t bsel;  // the chosen bucket's measure
+      if constexpr (MASS) {
+        bucket[lane] = 0;
+        wave_sync();
 #pragma unroll
-      for (int t = 0; t < NS; ++t) {
-        if (on(t) && f(t) && (c[t] >> (sh + 6)) == prefix)
-          atomicAdd((unsigned long long*)&bucket[63 - (int)((c[t] >> sh) & 63)], (unsigned long long)(MASS ? w[t] : 1ull));
+        for (int t = 0; t < NS; ++t) {
+          if (on(t) && f(t) && (c[t] >> (sh + 6)) == prefix)
+            atomicAdd((unsigned long long*)&bucket[63 - (int)((c[t] >> sh) & 63)], (unsigned long long)w[t]);
+        }
+        wave_sync();
+        const uint64_t bv = bucket[lane];
+        const uint64_t incl = wscan_incl_u64(bv);
+        const int sel = (int)__ffsll((long long)__ballot(incl >= target)) - 1;
+        target -= lane_u64(incl, sel) - lane_u64(bv, sel);
+        prefix = (prefix << 6) | (uint64_t)(63 - sel);
+        bsel = lane_u64(bv, sel);
+      } else {
+        // counts fit 32 bits: 32-bit buckets, atomics and scan
+        uint32_t* b32 = (uint32_t*)bucket;
+        b32[lane] = 0u;
+        wave_sync();
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+          if (on(t) && f(t) && (c[t] >> (sh + 6)) == prefix) atomicAdd(&b32[63 - (int)((c[t] >> sh) & 63)], 1u);
+        }
+        wave_sync();
+        const uint32_t bv = b32[lane];
+        const uint32_t incl = wscan_incl_u32(bv);
+        const int sel = (int)__ffsll((long long)__ballot((uint64_t)incl >= target)) - 1;
+        target -= (uint64_t)(lane_u32(incl, sel) - lane_u32(bv, sel));
+        prefix = (prefix << 6) | (uint64_t)(63 - sel);
+        bsel = lane_u32(bv, sel);
       }
-      wave_sync();
-      const uint64_t bv = bucket[lane];
-      const uint64_t incl = wscan_incl_u64(bv);
-      const int sel = (int)__ffsll((long long)__ballot(incl >= target)) - 1;
-      target -= lane_u64(incl, sel) - lane_u64(bv, sel);
-      prefix = (prefix << 6) | (uint64_t)(63 - sel);
       wave_sync();
       // counting, a chosen bucket of count one is the answer: the target lies
       // inside that bucket's measure
-      if (!MASS && sh > 0 && lane_u64(bv, sel) == 1ull) {
+      if (!MASS && sh > 0 && bsel == 1ull) {
         uint64_t only = 0;
 #pragma unroll
         for (int t = 0; t < NS; ++t) only |= (on(t) && f(t) && (c[t] >> sh) == prefix) ? c[t] : 0ull;
