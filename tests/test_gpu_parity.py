@@ -138,6 +138,31 @@ def test_random_parameters_parity(S, dev, oracle, seed):
         assert np.array_equal(tok, ot), engine
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_small_topk_then_topp(S, dev, oracle, seed):
+    """mlx_lm order with a small top-k before top-p: the register merge cuts
+    top-p over at most 64 alive candidates.  Quantised logits give dense value
+    ties (ids break them); kept-set sizes and tokens must match exactly."""
+    rng = np.random.default_rng(900 + seed)
+    B, V = 24, 151936
+    k = (8, 33, 64)[seed % 3]
+    top_p = (0.5, 0.8, 0.95)[seed // 2 % 3]
+    T = (0.7, 1.0)[seed % 2]
+    x = rng.normal(0.0, 2.5, (B, V))
+    if seed % 2 == 0:
+        x = np.round(x * 2) / 2  # many equal values among the top candidates
+    x[:, rng.choice(V, 12, replace=False)] += 6.0
+    x = x.astype(np.float32)
+    u = rng.random(B, dtype=np.float32)
+    p = oracle.make_params(B, temperature=T, top_p=top_p, top_k=k, min_p=0.0, chain=0)
+    ot, ok = oracle.sample(x, p, u, None, None)
+    announce(f"wh_sample small top-k then top-p seed={seed} k={k} p={top_p} T={T}")
+    tok, kept = S.sample(torch.from_numpy(x).to(dev), temperature=T, top_p=top_p, top_k=k, min_p=0.0, chain=0,
+                         uniforms=torch.from_numpy(u).to(dev), return_kept=True)
+    assert np.array_equal(kept.cpu().numpy(), ok)
+    assert np.array_equal(tok.cpu().numpy(), ot)
+
+
 @pytest.mark.parametrize("seed", range(3))
 def test_dense_block_and_ties_full_vocab(S, dev, oracle, seed):
     """Full-vocabulary rows built to reach the rarer steps of the register
