@@ -1069,7 +1069,7 @@ struct BlockStore {
   }
   // the caller has checked that more than k are kept
   __device__ __forceinline__ void keep_topk(int k) {
-    const uint64_t ck = radix_select<ORD_A, true, true>(src, pr, [](int, float) { return (uint64_t)1; }, (uint64_t)k, *sm);
+    const uint64_t ck = block_kth_desc<ORD_A>(src, pr, (uint64_t)k, *sm);
     pr.use_k = 1;
     pr.ck = ck;
   }

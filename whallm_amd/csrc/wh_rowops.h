@@ -237,6 +237,91 @@ __device__ uint64_t radix_select(const Src& src, const Pred& pr, Meas meas, uint
   return prefix;
 }
 
+// The composite (order ORD) of the k-th largest kept element (1 <= k <= the
+// kept count): the answer of radix_select<ORD> counting to target k.  Below
+// the bits every kept composite shares, 11-bit histogram passes (2048 32-bit
+// bins, atomics in LDS) narrow the prefix only until the chosen bin holds at
+// most 64 elements; those are gathered to an LDS list, and one wave ranks
+// them (each lane counts the listed composites above its own from broadcast
+// reads).  On continuous values one pass usually suffices, against the
+// radix descent's pass per 10 bits until a bin of count one.
+template <int ORD, typename Src>
+__device__ uint64_t block_kth_desc(const Src& src, const Pred& pr, uint64_t k, ExactSmem& sm) {
+  const int tid = threadIdx.x;
+  uint64_t cmin = ~0ull, cmax = 0;
+  src.each([&](int i, float l) {
+    if (!pr.keep(i, l)) return;
+    const uint64_t c = composite<ORD>(l, i);
+    cmin = c < cmin ? c : cmin;
+    cmax = c > cmax ? c : cmax;
+  });
+  cmin = block_reduce(cmin, sm.scratch64, OpMinU64(), (uint64_t)~0ull);
+  cmax = block_reduce(cmax, sm.scratch64, OpMaxU64(), (uint64_t)0);
+  if (cmax < cmin) return 0;
+  const uint64_t diff = cmin ^ cmax;
+  int sh = diff ? 64 - __clzll((long long)diff) : 0;  // composites differ only below bit sh
+  if (sh == 0) return cmax;
+  uint64_t prefix = sh >= 64 ? 0ull : cmax >> sh;
+  uint32_t* const h32 = (uint32_t*)sm.hist;  // 2048 bins
+  uint64_t* const lst = sm.hist;             // the gathered list (bins are dead by then)
+  uint64_t n_under = ~0ull;                  // kept elements under the prefix (unknown at first)
+  constexpr int NB = 2048;
+  const int per = NB / (int)blockDim.x;      // bins per thread, descending from top
+  const int top = NB - 1 - tid * per;
+  while (sh > 0 && n_under > 64) {
+    const int d = sh < 11 ? sh : 11;
+    sh -= d;
+    for (int i = tid; i < NB; i += blockDim.x) h32[i] = 0u;
+    __syncthreads();
+    src.each([&](int i, float l) {
+      if (!pr.keep(i, l)) return;
+      const uint64_t c = composite<ORD>(l, i);
+      if ((sh + d >= 64 ? 0ull : c >> (sh + d)) != prefix) return;
+      atomicAdd(&h32[(int)((c >> sh) & (uint64_t)((1 << d) - 1))], 1u);
+    });
+    __syncthreads();
+    uint64_t ls = 0;
+    for (int q = 0; q < per; ++q) ls += h32[top - q];
+    uint64_t tot;
+    uint64_t c = block_exclusive_scan_u64(ls, sm.scratch64, &tot);
+    if (c < k && c + ls >= k) {
+      for (int q = 0; q < per; ++q) {
+        const uint64_t hv = h32[top - q];
+        if (c < k && c + hv >= k) {
+          sm.bcast64[0] = (uint64_t)(top - q);
+          sm.bcast64[1] = c;
+          sm.bcast64[2] = hv;
+        }
+        c += hv;
+      }
+    }
+    __syncthreads();
+    prefix = (prefix << d) | sm.bcast64[0];
+    k -= sm.bcast64[1];
+    n_under = sm.bcast64[2];
+    __syncthreads();
+  }
+  if (sh == 0) return prefix;  // one composite is left: the prefix itself
+  // at most 64 kept elements under the prefix: list them, then one wave ranks
+  if (tid == 0) sm.bcasti[0] = 0;
+  __syncthreads();
+  src.each([&](int i, float l) {
+    if (!pr.keep(i, l)) return;
+    const uint64_t c = composite<ORD>(l, i);
+    if ((c >> sh) == prefix) lst[atomicAdd(&sm.bcasti[0], 1)] = c;
+  });
+  __syncthreads();
+  if (tid < 64) {
+    const int n = sm.bcasti[0];
+    const uint64_t mine = tid < n ? lst[tid] : 0ull;
+    uint64_t above = 0;
+    for (int j = 0; j < n; ++j) above += lst[j] > mine ? 1ull : 0ull;
+    if (tid < n && above == k - 1) sm.bcast64[3] = mine;
+  }
+  __syncthreads();
+  return sm.bcast64[3];
+}
+
 __device__ __forceinline__ float chain_scale(int chain, float d, float invT, double rTc) {
   return chain == WH_CHAIN_MLX ? d * invT : div_by_recip(d, rTc);
 }
