@@ -1421,8 +1421,10 @@ __device__ __noinline__ int merge_block(const SampleKArgs* ap, const FastPlan* p
   st.pr = Pred{0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
   st.m = m;
   st.sm = &sm;
-  const uint64_t Scand = st.mass(false, 0.0f);
-  const ZBounds zb = z_bounds_loop(hd, G, m, Scand);
+  // the normaliser bounds serve the top-p cut alone (rp.use_p is uniform
+  // over the workgroup, so the block reductions inside run on every thread)
+  ZBounds zb{0ull, 0ull};
+  if (rp.use_p) zb = z_bounds_loop(hd, G, m, st.mass(false, 0.0f));
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
   const float invT = (float)(1.0 / (double)rp.T);
   const double rTc = 1.0 / (double)(float)fmax((double)rp.T, 1e-5);
