@@ -1431,39 +1431,12 @@ __device__ __noinline__ int merge_block(const SampleKArgs* ap, const FastPlan* p
   const Pred pr = st.pr;
   const CandSource src = st.src;
   auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, rTc)); };
-  uint64_t zv = 0;
-  int nk = 0;
-  src.each([&](int i, float l) {
-    if (pr.keep(i, l)) {
-      zv += vw(i, l);
-      ++nk;
-    }
-  });
-  // the two sums in one block reduction (one pair of barriers)
-  const int lane = tid & 63, wv = tid >> 6, nw = nt >> 6;
-  zv = wsum_u64(zv);
-  nk = wsum_i(nk);
-  __syncthreads();
-  if (lane == 0) {
-    sm.scratch64[wv] = zv;
-    sm.scratchi[wv] = nk;
-  }
-  __syncthreads();
-  uint64_t ZV = 0;
-  int nkept = 0;
-  for (int w = 0; w < nw; ++w) {
-    ZV += sm.scratch64[w];
-    nkept += sm.scratchi[w];
-  }
-  if (a.tokens) {
-    int tok = 0;
-    if (ZV) {
-      const uint64_t tgt = draw_target(ub, ZV);
-      // ids have 18 bits: two 10-bit passes, no common-prefix pass
-      tok = 0x3FFFF - (int)radix_select<ORD_ID>(src, pr, vw, tgt + 1, sm);
-    }
-    if (tid == 0) a.tokens[b] = tok;
-  }
+  // the draw weights' sum, the kept count and the draw in one pass plus the
+  // target's bin
+  uint64_t ZV;
+  int nkept;
+  const int tok = block_draw_id(src, pr, vw, ub, a.tokens != nullptr, sm, &ZV, &nkept);
+  if (tid == 0 && a.tokens) a.tokens[b] = tok;
   if (tid == 0 && a.kept) a.kept[b] = nkept;
   float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
   if (out) {

@@ -322,6 +322,76 @@ __device__ uint64_t block_kth_desc(const Src& src, const Pred& pr, uint64_t k, E
   return sm.bcast64[3];
 }
 
+// The categorical draw over the kept elements in vocabulary order, with the
+// normaliser and the kept count: returns the first id whose inclusive weight
+// sum exceeds draw_target(u, ZV) (0 when ZV = 0 or want_tok is false), where
+// ZV = the kept weights' sum.  One pass adds every kept weight into 1024
+// bins of 256 ids; the scan's total is ZV, and the bin holding the target
+// has at most 256 kept elements.  Those are listed in LDS, and each thread
+// holding one sums the listed weights at or below its id: the answer is the
+// element whose inclusive sum passes the remainder while its exclusive sum
+// does not.  Ids must lie below 2^18.
+template <typename Src, typename WF>
+__device__ int block_draw_id(const Src& src, const Pred& pr, WF vw, float u, bool want_tok, ExactSmem& sm,
+                             uint64_t* ZV_out, int* nk_out) {
+  const int tid = threadIdx.x;
+  constexpr int NB = 1024;
+  const int per = NB / (int)blockDim.x;  // bins per thread, ascending from b0
+  const int b0 = tid * per;
+  for (int i = tid; i < NB; i += blockDim.x) sm.hist[i] = 0;
+  __syncthreads();
+  int nk = 0;
+  src.each([&](int i, float l) {
+    if (!pr.keep(i, l)) return;
+    ++nk;
+    const uint64_t w = vw(i, l);
+    if (w) atomicAdd((unsigned long long*)&sm.hist[i >> 8], (unsigned long long)w);
+  });
+  __syncthreads();
+  uint64_t ls = 0;
+  for (int q = 0; q < per; ++q) ls += sm.hist[b0 + q];
+  uint64_t ZV;
+  uint64_t c = block_exclusive_scan_u64(ls, sm.scratch64, &ZV);
+  *ZV_out = ZV;
+  *nk_out = block_reduce(nk, sm.scratchi, OpSumI(), 0);
+  if (!want_tok || ZV == 0) return 0;
+  const uint64_t tgt = draw_target(u, ZV);  // < ZV
+  if (c <= tgt && tgt < c + ls) {
+    for (int q = 0; q < per; ++q) {
+      const uint64_t hv = sm.hist[b0 + q];
+      if (c <= tgt && tgt < c + hv) {
+        sm.bcast64[0] = (uint64_t)(b0 + q);
+        sm.bcast64[1] = c;
+      }
+      c += hv;
+    }
+  }
+  __syncthreads();
+  const int bin = (int)sm.bcast64[0];
+  const uint64_t rem = tgt - sm.bcast64[1];  // inside the bin's weight
+  if (tid == 0) sm.bcasti[0] = 0;
+  __syncthreads();
+  // the bin's kept elements (at most 256) as (weight, id) in the dead bins
+  uint64_t* const lw = sm.hist;
+  int* const lid = (int*)(sm.hist + 256);
+  src.each([&](int i, float l) {
+    if (!pr.keep(i, l) || (i >> 8) != bin) return;
+    const int at = atomicAdd(&sm.bcasti[0], 1);
+    lw[at] = vw(i, l);
+    lid[at] = i;
+  });
+  __syncthreads();
+  const int n = sm.bcasti[0];
+  for (int t = tid; t < n; t += blockDim.x) {
+    const int me = lid[t];
+    uint64_t incl = 0;
+    for (int j = 0; j < n; ++j) incl += lid[j] <= me ? lw[j] : 0ull;
+    if (incl > rem && incl - lw[t] <= rem) sm.bcasti[1] = me;
+  }
+  __syncthreads();
+  return sm.bcasti[1];
+}
+
 __device__ __forceinline__ float chain_scale(int chain, float d, float invT, double rTc) {
   return chain == WH_CHAIN_MLX ? d * invT : div_by_recip(d, rTc);
 }
