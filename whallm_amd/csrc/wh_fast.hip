@@ -964,6 +964,9 @@ struct RegStore {
     const uint64_t ck = select_desc<ORD_A, false>([](int) { return true; }, (uint64_t)k, bkt);
     keep_if([&](int t) { return comp_a(fkey(cl[t]), ci[t]) >= ck; });
   }
+  __device__ __forceinline__ void topk_filter(int k) {
+    if (count() > k) keep_topk(k);
+  }
   // Top-p cut over the alive covered slots: both ends of [Rlo, Rhi] must
   // select the same element (order P).
   __device__ __forceinline__ bool keep_pcut(uint64_t Rlo, uint64_t Rhi, float tcov) {
@@ -1067,11 +1070,14 @@ struct BlockStore {
     pr.use_m = 1;
     pr.thr = thr;
   }
-  // the caller has checked that more than k are kept
-  __device__ __forceinline__ void keep_topk(int k) {
-    const uint64_t ck = block_kth_desc<ORD_A>(src, pr, (uint64_t)k, *sm);
-    pr.use_k = 1;
-    pr.ck = ck;
+  // top-k when more than k are kept (the count comes from the select's
+  // first pass)
+  __device__ __forceinline__ void topk_filter(int k) {
+    uint64_t ck;
+    if (block_kth_desc<ORD_A>(src, pr, (uint64_t)k, *sm, &ck)) {
+      pr.use_k = 1;
+      pr.ck = ck;
+    }
   }
   __device__ __forceinline__ bool keep_pcut(uint64_t Rlo, uint64_t Rhi, float tcov) {
     Pred pc = pr;
@@ -1127,7 +1133,7 @@ __device__ __forceinline__ bool run_filters(St& st, const SampleKArgs& a, const 
   const float thr = m + min_p_log(a, rp.min_p);
   if (a.chain == WH_CHAIN_MLX && rp.use_k && rp.use_p) {
     // k -> p -> min-p; the candidates hold the whole top-k set
-    if (st.count() > rp.top_k) st.keep_topk(rp.top_k);
+    st.topk_filter(rp.top_k);
     if (!apply_p(true)) return false;
     if (!none && rp.use_m) st.keep_min(thr);
   } else {
@@ -1135,7 +1141,7 @@ __device__ __forceinline__ bool run_filters(St& st, const SampleKArgs& a, const 
     // k -> min-p keeps the first k of the min-p set, which is a value prefix
     if (rp.use_p && !apply_p(false)) return false;
     if (!none && rp.use_m) st.keep_min(thr);
-    if (!none && rp.use_k && st.count() > rp.top_k) st.keep_topk(rp.top_k);
+    if (!none && rp.use_k) st.topk_filter(rp.top_k);
   }
   return true;
 }

@@ -237,8 +237,9 @@ __device__ uint64_t radix_select(const Src& src, const Pred& pr, Meas meas, uint
   return prefix;
 }
 
-// The composite (order ORD) of the k-th largest kept element (1 <= k <= the
-// kept count): the answer of radix_select<ORD> counting to target k.  Below
+// The composite (order ORD) of the k-th largest kept element, the answer of
+// radix_select<ORD> counting to target k (k >= 1), in *cut; false (no cut)
+// when at most k elements are kept.  Below
 // the bits every kept composite shares, 11-bit histogram passes (2048 32-bit
 // bins, atomics in LDS) narrow the prefix only until the chosen bin holds at
 // most 64 elements; those are gathered to an LDS list, and one wave ranks
@@ -246,25 +247,31 @@ __device__ uint64_t radix_select(const Src& src, const Pred& pr, Meas meas, uint
 // reads).  On continuous values one pass usually suffices, against the
 // radix descent's pass per 10 bits until a bin of count one.
 template <int ORD, typename Src>
-__device__ uint64_t block_kth_desc(const Src& src, const Pred& pr, uint64_t k, ExactSmem& sm) {
+__device__ bool block_kth_desc(const Src& src, const Pred& pr, uint64_t k, ExactSmem& sm, uint64_t* cut) {
   const int tid = threadIdx.x;
   uint64_t cmin = ~0ull, cmax = 0;
+  int cnt = 0;
   src.each([&](int i, float l) {
     if (!pr.keep(i, l)) return;
     const uint64_t c = composite<ORD>(l, i);
     cmin = c < cmin ? c : cmin;
     cmax = c > cmax ? c : cmax;
+    ++cnt;
   });
+  cnt = block_reduce(cnt, sm.scratchi, OpSumI(), 0);
+  if ((uint64_t)cnt <= k) return false;
   cmin = block_reduce(cmin, sm.scratch64, OpMinU64(), (uint64_t)~0ull);
   cmax = block_reduce(cmax, sm.scratch64, OpMaxU64(), (uint64_t)0);
-  if (cmax < cmin) return 0;
   const uint64_t diff = cmin ^ cmax;
   int sh = diff ? 64 - __clzll((long long)diff) : 0;  // composites differ only below bit sh
-  if (sh == 0) return cmax;
+  if (sh == 0) {
+    *cut = cmax;
+    return true;
+  }
   uint64_t prefix = sh >= 64 ? 0ull : cmax >> sh;
   uint32_t* const h32 = (uint32_t*)sm.hist;  // 2048 bins
   uint64_t* const lst = sm.hist;             // the gathered list (bins are dead by then)
-  uint64_t n_under = ~0ull;                  // kept elements under the prefix (unknown at first)
+  uint64_t n_under = (uint64_t)cnt;          // kept elements under the prefix
   constexpr int NB = 2048;
   const int per = NB / (int)blockDim.x;      // bins per thread, descending from top
   const int top = NB - 1 - tid * per;
@@ -301,7 +308,10 @@ __device__ uint64_t block_kth_desc(const Src& src, const Pred& pr, uint64_t k, E
     n_under = sm.bcast64[2];
     __syncthreads();
   }
-  if (sh == 0) return prefix;  // one composite is left: the prefix itself
+  if (sh == 0) {  // one composite is left: the prefix itself
+    *cut = prefix;
+    return true;
+  }
   // at most 64 kept elements under the prefix: list them, then one wave ranks
   if (tid == 0) sm.bcasti[0] = 0;
   __syncthreads();
@@ -319,7 +329,8 @@ __device__ uint64_t block_kth_desc(const Src& src, const Pred& pr, uint64_t k, E
     if (tid < n && above == k - 1) sm.bcast64[3] = mine;
   }
   __syncthreads();
-  return sm.bcast64[3];
+  *cut = sm.bcast64[3];
+  return true;
 }
 
 // The categorical draw over the kept elements in vocabulary order, with the
