@@ -1043,9 +1043,9 @@ __device__ __forceinline__ ZBounds z_bounds_loop(const SliceHdr* hd, int G, floa
   return z_finish(s, Scand);
 }
 
-// Candidates in LDS (any number), filtered by the whole workgroup: counts and
-// masses are block reductions, cut points block radix selects.  Every method
-// is called by every thread.
+// Candidates in LDS (any number), filtered by the whole workgroup: masses are
+// block reductions, the top-k cut a histogram-then-rank select, the top-p cut
+// block radix selects.  Every method is called by every thread.
 struct BlockStore {
   CandSource src;
   Pred pr;

@@ -162,11 +162,7 @@ __device__ __forceinline__ uint64_t composite(float l, int i) {
 // short candidate lists, whose composites often share their top bits), one
 // min/max pass first drops the digits every kept composite shares, which
 // would otherwise send every atomic of a pass to one bin.
-//
-// ONES: the measure is 1 for every kept element (a count).  A chosen bin of
-// count one then holds the answer, and one pass finds it in place of the
-// remaining histogram passes.
-template <int ORD, bool SKIP = false, bool ONES = false, typename Src, typename Meas>
+template <int ORD, bool SKIP = false, typename Src, typename Meas>
 __device__ uint64_t radix_select(const Src& src, const Pred& pr, Meas meas, uint64_t target, ExactSmem& sm) {
   const int tid = threadIdx.x;
   int PASSES = ORD == ORD_ID ? 2 : 5;
@@ -220,19 +216,7 @@ __device__ uint64_t radix_select(const Src& src, const Pred& pr, Meas meas, uint
     __syncthreads();
     prefix = (prefix << 10) | sm.bcast64[0];
     target -= sm.bcast64[1];
-    const bool single = ONES && shift > 0 && sm.hist[sm.bcast64[0]] == 1ull;
     __syncthreads();
-    if (single) {
-      src.each([&](int i, float l) {
-        if (!pr.keep(i, l)) return;
-        const uint64_t c = composite<ORD>(l, i);
-        if ((c >> shift) == prefix) sm.bcast64[2] = c;
-      });
-      __syncthreads();
-      const uint64_t c = sm.bcast64[2];
-      __syncthreads();
-      return c;
-    }
   }
   return prefix;
 }
