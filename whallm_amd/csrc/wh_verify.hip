@@ -417,11 +417,12 @@ __global__ void __launch_bounds__(VT1) verify_sum_kernel(VerifyKArgs a, VPlan P)
 // Row j's max and the proven interval of its fixed-point normaliser, from
 // its slice summaries.  Every lane of a full wave calls it; lane l < G1
 // passes slice l's summary (valid), and every lane gets the results.
-__device__ __forceinline__ void vrow_bounds_w(const VRowSum& r, bool valid, float Tc, int V, float* m_out,
+__device__ __forceinline__ void vrow_bounds_w(const VRowSum& r, bool valid, float iT, int V, float* m_out,
                                               uint64_t* zlo, uint64_t* zhi) {
   const float m = wmax_f(valid ? r.m : -INFINITY);
-  // the float rescale's relative error (a few ulp) is far inside VEPS
-  const double t = (valid && m != -INFINITY && r.m != -INFINITY) ? r.zf * (double)__expf((r.m - m) / Tc) : 0.0;
+  // the float rescale's relative error (a few ulp, with iT = fl(1 / T)) is
+  // far inside VEPS
+  const double t = (valid && m != -INFINITY && r.m != -INFINITY) ? r.zf * (double)__expf((r.m - m) * iT) : 0.0;
   const double zf = wsum_f64(t);
   const double SC = 17592186044416.0, LIM = 4.0e18;
   const double lo = zf * SC * (1.0 - VEPS) - (double)V, hi = zf * SC * (1.0 + VEPS) + (double)V;
@@ -478,7 +479,7 @@ __global__ void __launch_bounds__(VT2) verify_prep_kernel(VerifyKArgs a, VPlan P
     if (j <= n) {
       float m;
       uint64_t zlo, zhi;
-      vrow_bounds_w(r[q], lane < G1, a.Tc, V, &m, &zlo, &zhi);
+      vrow_bounds_w(r[q], lane < G1, (float)a.rTc, V, &m, &zlo, &zhi);
       if (lane == q) {
         s_m[j] = m;
         if (j < n) {
