@@ -280,7 +280,7 @@ __device__ __forceinline__ void ladder_count(const float (&gm)[R], const int2* p
 //   k > 0 (top-k bound): a threshold with at least k slice elements at or
 //     above it -- the highest rung whose group count reaches k (each counted
 //     group holds at least one such element), refined while the count
-//     exceeds max(2k, 64).  When no rung reaches k (an outlier far above the
+//     exceeds max(1.5 k, 64).  When no rung reaches k (an outlier far above the
 //     rest of the slice), a second round tries 2^11 .. 2^18 below the max;
 //     -inf when that fails too.
 //   k <= 0 (top-p alone): the lowest rung whose group count is at most half
@@ -299,7 +299,7 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
   ladder_count<R>(gm, patch, npatch, x, c, 0, sm);
   if (k > 0) {
     // counts grow with j: hi = last rung with count < k, lo = first with >= k
-    const int target = max(2 * k, 64);
+    const int target = max(k + k / 2, 64);
     bool found = false;
     float lo = -INFINITY, hi = INFINITY;
     int clo = 0;
