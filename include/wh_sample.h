@@ -77,14 +77,27 @@ typedef struct wh_sample_args {
 
   const float* uniforms;     /* device, [B] in [0,1); nullable only when tokens is NULL */
 
-  float temperature;         /* scalar parameters, overridden per row where the */
-  float top_p;               /* matching *_rows pointer is non-NULL            */
-  float min_p;
+  /* Scalar parameters, overridden per row where the matching *_rows pointer
+   * is non-NULL.  temperature, top_p and min_p are doubles: the reference's
+   * callers pass Python floats, and the float32 constants the filters use are
+   * derived from them as MLX derives them -- fp32(1 - top_p), fp32(1 / T),
+   * fp32(max(T, 1e-5)), fp32(ln min_p) -- so a value such as top_p = 0.9
+   * gives the same threshold (0.1f) as the reference, not fp32(1 - fp32(0.9)). */
+  double temperature;
+  double top_p;
+  double min_p;
   int32_t top_k;
-  const float* temperature_rows; /* device, nullable */
-  const float* top_p_rows;       /* device, nullable */
-  const float* min_p_rows;       /* device, nullable */
-  const int32_t* top_k_rows;     /* device, nullable; k >= V is a no-op */
+  int32_t history_share;     /* logits rows per history row: row b reads history row
+                                b / history_share (0 and 1: one history row each).
+                                MTP verification (qwen4_exp.py:1083-1092) penalises
+                                position i of a batch entry over history + drafts[:i]:
+                                its n+1 rows share one history row holding the
+                                committed ids followed by the drafts, with
+                                history_len = committed + i per row. */
+  const double* temperature_rows; /* device, nullable */
+  const double* top_p_rows;       /* device, nullable */
+  const double* min_p_rows;       /* device, nullable */
+  const int32_t* top_k_rows;      /* device, nullable; k >= V is a no-op */
 
   float repetition_penalty;  /* 0 = processor absent (1.0 is a no-op) */
   float presence_penalty;    /* 0 = absent */

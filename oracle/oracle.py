@@ -21,12 +21,14 @@ _LIB_PATH = os.path.join(_HERE, "build", "libwh_oracle.so")
 CHAIN_KPM = 0  # mlx_lm make_sampler: top_k -> top_p -> min_p, logprobs * (1/T)
 CHAIN_PMK = 1  # Whallm sampling_logprobs: top_p -> min_p -> top_k, logprobs / max(T, 1e-5)
 
+# who_params: temperature, top_p and min_p are the caller's doubles, as the
+# reference's Python floats are.
 PARAMS_DTYPE = np.dtype(
     [
-        ("temperature", np.float32),
-        ("top_p", np.float32),
+        ("temperature", np.float64),
+        ("top_p", np.float64),
+        ("min_p", np.float64),
         ("top_k", np.int32),
-        ("min_p", np.float32),
         ("repetition_penalty", np.float32),
         ("presence_penalty", np.float32),
         ("frequency_penalty", np.float32),
@@ -34,10 +36,9 @@ PARAMS_DTYPE = np.dtype(
         ("presence_context", np.int32),
         ("frequency_context", np.int32),
         ("chain", np.int32),
-        ("pad", np.int32),
     ]
 )
-assert PARAMS_DTYPE.itemsize == 48
+assert PARAMS_DTYPE.itemsize == 56
 
 _lib = None
 

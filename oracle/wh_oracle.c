@@ -51,10 +51,14 @@
 typedef unsigned __int128 u128;
 
 typedef struct {
-  float temperature;
-  float top_p;
+  /* temperature, top_p and min_p are the caller's doubles (Python floats in
+   * the reference); the float32 constants of the filters are derived from
+   * them as MLX derives them: fp32(1 - top_p), fp32(1 / T), fp32(max(T, 1e-5)),
+   * fp32(ln min_p). */
+  double temperature;
+  double top_p;
+  double min_p;
   int32_t top_k;
-  float min_p;
   float repetition_penalty; /* 0 => processor absent */
   float presence_penalty;   /* 0 => processor absent */
   float frequency_penalty;  /* 0 => processor absent */
@@ -62,7 +66,6 @@ typedef struct {
   int32_t presence_context;
   int32_t frequency_context;
   int32_t chain;
-  int32_t pad;
 } who_params;
 
 /* ------------------------------------------------------------------------ */
@@ -277,28 +280,28 @@ static void who_top_p(who_ws* ws, float theta, uint64_t Z) {
 }
 
 /* min-p: keep alive i iff l_i >= fl(max_alive + fl32(ln min_p)). */
-static void who_min_p(who_ws* ws, float min_p) {
+static void who_min_p(who_ws* ws, double min_p) {
   float mx = -INFINITY;
   for (int i = 0; i < ws->V; ++i) if (ws->alive[i] && ws->l[i] > mx) mx = ws->l[i];
-  float c = (float)log((double)min_p);
+  float c = (float)log(min_p);
   float thr = mx + c;
   for (int i = 0; i < ws->V; ++i) if (ws->alive[i] && !(ws->l[i] >= thr)) ws->alive[i] = 0;
 }
 
 /* The chain's float32 temperature scalings (reference: logits * (1/temp) in
  * make_sampler; logprobs / max(temperature, 1e-5) in sampling_logprobs). */
-static float who_scale(int chain, float d, float temperature) {
-  if (chain == WHO_CHAIN_KPM) return d * (float)(1.0 / (double)temperature);
-  return d / (float)fmax((double)temperature, 1e-5);
+static float who_scale(int chain, float d, double temperature) {
+  if (chain == WHO_CHAIN_KPM) return d * (float)(1.0 / temperature);
+  return d / (float)fmax(temperature, 1e-5);
 }
 
 /* Validate the same ranges mlx_lm / Whallm reject. */
 static int who_check(const who_params* p, int V) {
   if (p->chain != WHO_CHAIN_KPM && p->chain != WHO_CHAIN_PMK) return WHO_EINVAL;
-  if (!(p->temperature >= 0.0f)) return WHO_EINVAL;
-  if (!(p->min_p >= 0.0f && p->min_p <= 1.0f)) return WHO_EINVAL;
+  if (!(p->temperature >= 0.0)) return WHO_EINVAL;
+  if (!(p->min_p >= 0.0 && p->min_p <= 1.0)) return WHO_EINVAL;
   if (p->repetition_penalty < 0.0f) return WHO_EINVAL;
-  if (p->chain == WHO_CHAIN_KPM && p->temperature > 0.0f && p->top_k > 0 && p->top_k >= V) return WHO_EINVAL;
+  if (p->chain == WHO_CHAIN_KPM && p->temperature > 0.0 && p->top_k > 0 && p->top_k >= V) return WHO_EINVAL;
   if (p->top_k < 0) return WHO_EINVAL;
   return WHO_OK;
 }
@@ -312,7 +315,7 @@ static int who_contract_row(who_ws* ws, const float* x, const int32_t* h, int hl
   for (int i = 0; i < V; ++i) l[i] = x[i] + 0.0f; /* -0 -> +0 */
   who_penalize(l, V, h, hlen, p, ws->cnt);
   for (int i = 0; i < V; ++i) l[i] = l[i] + 0.0f;
-  if (p->temperature == 0.0f) {
+  if (p->temperature == 0.0) {
     if (kept_out) *kept_out = 1;
     if (out_row) memcpy(out_row, l, sizeof(float) * V);
     return who_argmax(l, V);
@@ -325,10 +328,10 @@ static int who_contract_row(who_ws* ws, const float* x, const int32_t* h, int hl
     ws->alive[i] = 1;
   }
   who_sort_desc(l, ws->ord, V);
-  float theta = (float)(1.0 - (double)p->top_p);
+  float theta = (float)(1.0 - p->top_p);
   int use_k = p->top_k > 0 && p->top_k < V;
-  int use_p = p->top_p > 0.0f && p->top_p < 1.0f;
-  int use_m = p->min_p != 0.0f;
+  int use_p = p->top_p > 0.0 && p->top_p < 1.0;
+  int use_m = p->min_p != 0.0;
   if (p->chain == WHO_CHAIN_KPM) {
     if (use_k) who_top_k(ws, p->top_k);
     if (use_p) who_top_p(ws, theta, Z);
@@ -610,19 +613,25 @@ static int who_cmp_desc_stable(const void* a, const void* b) {
   return (i > j) - (i < j);
 }
 
-/* inverse-CDF draw in float32 from a logprob-like row (entries -inf excluded) */
+/* Inverse-CDF draw from a logprob-like row (entries -inf excluded).  The
+ * reference draws by Gumbel-max (mx.random.categorical, dspark.py:329, 904),
+ * which has no cumulative sum; a uniform-driven replay needs one, and it is
+ * accumulated in float64 over the row's float32 weights expf(z - max) so the
+ * draw adds no rounding of its own: a float32 sequential sum over a
+ * 129,280-id residual row drifts by ~1e-5, far above the row's own float32
+ * rounding. */
 static int who_draw_f32(const float* z, int V, float u) {
   float m = -INFINITY;
   for (int i = 0; i < V; ++i) if (z[i] > m) m = z[i];
   if (m == -INFINITY) return 0;
-  float tot = 0.0f;
-  for (int i = 0; i < V; ++i) tot += expf(z[i] - m);
-  float tgt = u * tot, c = 0.0f;
+  double tot = 0.0;
+  for (int i = 0; i < V; ++i) tot += (double)expf(z[i] - m);
+  double tgt = (double)u * tot, c = 0.0;
   int last = 0;
   for (int i = 0; i < V; ++i) {
     float w = expf(z[i] - m);
     if (w == 0.0f) continue;
-    c += w;
+    c += (double)w;
     last = i;
     if (c > tgt) return i;
   }
@@ -643,7 +652,7 @@ static int who_faithful_row(who_fws* ws, int V, const float* x, const int32_t* h
   float* lp = ws->lp;
   memcpy(l, x, sizeof(float) * V);
   who_penalize(l, V, h, hlen, p, ws->cnt);
-  if (p->temperature == 0.0f) {
+  if (p->temperature == 0.0) {
     if (kept_out) *kept_out = 1;
     if (p->chain == WHO_CHAIN_PMK) {
       if (out_row) memcpy(out_row, l, sizeof(float) * V);
@@ -656,10 +665,10 @@ static int who_faithful_row(who_fws* ws, int V, const float* x, const int32_t* h
   float lse = who_lse_f32(l, V);
   for (int i = 0; i < V; ++i) lp[i] = l[i] - lse;
   int use_k = p->top_k > 0 && p->top_k < V;
-  int use_p = p->top_p > 0.0f && p->top_p < 1.0f;
-  int use_m = p->min_p != 0.0f;
-  float theta = (float)(1.0 - (double)p->top_p);
-  float cmin = (float)log((double)p->min_p);
+  int use_p = p->top_p > 0.0 && p->top_p < 1.0;
+  int use_m = p->min_p != 0.0;
+  float theta = (float)(1.0 - p->top_p);
+  float cmin = (float)log(p->min_p);
   for (int s = 0; s < 3; ++s) {
     int step = p->chain == WHO_CHAIN_KPM ? s : (s + 1) % 3; /* KPM: k,p,m ; PMK: p,m,k */
     if (step == 0 && use_k) {
@@ -689,11 +698,11 @@ static int who_faithful_row(who_fws* ws, int V, const float* x, const int32_t* h
   for (int i = 0; i < V; ++i) nk += lp[i] != -INFINITY;
   if (kept_out) *kept_out = nk;
   if (p->chain == WHO_CHAIN_KPM) {
-    float inv = (float)(1.0 / (double)p->temperature);
+    float inv = (float)(1.0 / p->temperature);
     for (int i = 0; i < V; ++i) lp[i] = lp[i] * inv;
     return who_draw_f32(lp, V, u);
   }
-  float Tc = (float)fmax((double)p->temperature, 1e-5);
+  float Tc = (float)fmax(p->temperature, 1e-5);
   for (int i = 0; i < V; ++i) lp[i] = lp[i] / Tc;
   float l2 = who_lse_f32(lp, V);
   for (int i = 0; i < V; ++i) lp[i] = lp[i] - l2;

@@ -41,19 +41,23 @@ def test_library_exports_every_declared_symbol(L):
 
 
 def test_struct_layouts_match_ctypes(L, tmp_path):
+    """Every field's offset and both structs' sizes, from gcc on the header,
+    against the ctypes mirror."""
+    lines = []
+    for cname, cls in (("wh_sample_args", L.SampleArgs), ("wh_verify_args", L.VerifyArgs)):
+        lines.append(f'printf("%zu\\n", sizeof({cname}));')
+        for f in cls._fields_:
+            lines.append(f'printf("%zu\\n", offsetof({cname}, {f[0]}));')
     prog = tmp_path / "layout.c"
-    prog.write_text(
-        '#include <stdio.h>\n#include <stddef.h>\n#include "wh_sample.h"\n'
-        "int main(void){printf(\"%zu %zu %zu %zu %zu %zu %zu\\n\", sizeof(wh_sample_args),"
-        " offsetof(wh_sample_args, uniforms), offsetof(wh_sample_args, top_k_rows),"
-        " offsetof(wh_sample_args, out_mode), offsetof(wh_sample_args, workspace_bytes),"
-        " sizeof(wh_verify_args), offsetof(wh_verify_args, row_out)); return 0;}\n")
+    prog.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "wh_sample.h"\nint main(void){'
+                    + "".join(lines) + "return 0;}\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(prog), "-o", str(exe)], check=True)
     got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()))
-    S, Vr = L.SampleArgs, L.VerifyArgs
-    want = [ctypes.sizeof(S), S.uniforms.offset, S.top_k_rows.offset, S.out_mode.offset, S.workspace_bytes.offset,
-            ctypes.sizeof(Vr), Vr.row_out.offset]
+    want = []
+    for cls in (L.SampleArgs, L.VerifyArgs):
+        want.append(ctypes.sizeof(cls))
+        want += [getattr(cls, f[0]).offset for f in cls._fields_]
     assert got == want
 
 

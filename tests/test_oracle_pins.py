@@ -415,17 +415,3 @@ def test_verify_zero_residual_falls_back_to_target(oracle):
     acc, tok = oracle.verify_logprobs(q[None, None], np.stack([p, p])[None], np.array([[4]]),
                                       np.array([[0.5, 0.75]], np.float32), 1.0)
     assert acc[0] == 0 and tok[0] in (2, 3)
-
-
-def test_faithful_and_contract_agree_away_from_boundaries(oracle):
-    rng = np.random.default_rng(9)
-    B, V = 64, 4000
-    x = rng.normal(0, 3, (B, V)).astype(np.float32)
-    hist = rng.integers(0, V, (B, 256)).astype(np.int32)
-    p = oracle.make_params(B, temperature=1.0, top_p=0.9, min_p=0.05, presence_penalty=0.5,
-                           frequency_penalty=0.3, chain=0)
-    u = rng.random(B, dtype=np.float32)
-    a, ka = oracle.sample(x, p, u, hist)
-    b, kb = oracle.sample_faithful(x, p, u, hist)
-    assert np.mean(a == b) >= 0.95
-    assert np.mean(ka == kb) >= 0.95

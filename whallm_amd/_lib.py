@@ -32,6 +32,7 @@ _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
+_f64 = ctypes.c_double
 
 
 class SampleArgs(ctypes.Structure):
@@ -39,7 +40,7 @@ class SampleArgs(ctypes.Structure):
         ("logits", _p), ("dtype", _i32), ("B", _i32), ("V", _i32), ("chain", _i32), ("row_stride", _i64),
         ("history", _p), ("history_stride", _i64), ("history_len", _p),
         ("uniforms", _p),
-        ("temperature", _f32), ("top_p", _f32), ("min_p", _f32), ("top_k", _i32),
+        ("temperature", _f64), ("top_p", _f64), ("min_p", _f64), ("top_k", _i32), ("history_share", _i32),
         ("temperature_rows", _p), ("top_p_rows", _p), ("min_p_rows", _p), ("top_k_rows", _p),
         ("repetition_penalty", _f32), ("presence_penalty", _f32), ("frequency_penalty", _f32),
         ("repetition_context", _i32), ("presence_context", _i32), ("frequency_context", _i32),

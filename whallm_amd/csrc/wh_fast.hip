@@ -96,10 +96,14 @@ struct FastPlan {
 };
 
 struct RowParams {
-  float T, top_p, min_p;
+  float theta;   // fl32(1 - top_p): the top-p threshold as MLX forms it from a double
+  float cmin;    // fl32(ln min_p)
+  float invT;    // fl32(1 / T): chain MLX scales the logprobs by it
+  double rTc;    // 1 / fl32(max(T, 1e-5)): chain WHALLM divides by fl32(max(T, 1e-5))
   int top_k;
   bool use_k, use_p, use_m;
   bool greedy;
+  bool tscale;   // T != 1: the draw weights differ from the masses
   bool tk;   // tau from the slice's k-th value
   bool tm;   // tau from min-p
   bool tp;   // tau from the candidate capacity (top-p is the only filter that bounds)
@@ -118,6 +122,7 @@ struct SliceKernArgs {
   long long row_stride;  // elements
   int G, SL, V, hs;      // hs: history row stride
   int pen;               // penalties on
+  int hshare;            // logits rows per history row
   SampleKArgs a;
   FastPlan p;
 };
@@ -142,33 +147,39 @@ __device__ __forceinline__ const MergeKernArgs* merge_kernargs() {
 // The row's raw parameters: one unconditional load each, from the per-row
 // array or the scalar field (no branch join that waits for the load).
 struct RowRaw {
-  float T, top_p, min_p;
+  double T, top_p, min_p;
   int top_k;
 };
 // The loads go through the constant address space: the addresses are
 // uniform and the data is read-only for the kernel's lifetime, so they are
 // scalar loads, counted apart from the vector loads of the logits.
-typedef __attribute__((address_space(4))) const float cfloat;
+typedef __attribute__((address_space(4))) const double cdouble;
 typedef __attribute__((address_space(4))) const int cint;
 // ka is the kernel's own argument copy (in its argument segment).
 __device__ __forceinline__ RowRaw row_raw(const SampleKArgs& a, const SampleKArgs& ka, int b) {
   RowRaw r;
-  r.T = *(cfloat*)(a.T_rows ? a.T_rows + b : &ka.T);
-  r.top_p = *(cfloat*)(a.top_p_rows ? a.top_p_rows + b : &ka.top_p);
-  r.min_p = *(cfloat*)(a.min_p_rows ? a.min_p_rows + b : &ka.min_p);
+  r.T = *(cdouble*)(a.T_rows ? a.T_rows + b : &ka.T);
+  r.top_p = *(cdouble*)(a.top_p_rows ? a.top_p_rows + b : &ka.top_p);
+  r.min_p = *(cdouble*)(a.min_p_rows ? a.min_p_rows + b : &ka.min_p);
   r.top_k = *(cint*)(a.top_k_rows ? a.top_k_rows + b : &ka.top_k);
   return r;
 }
+// The float32 constants of the filters, derived from the caller's doubles
+// the way MLX derives them from Python floats (the scalar is rounded to the
+// array's float32 type after the double arithmetic).  Unused ones are dead
+// code in the kernels that do not need them.
 __device__ __forceinline__ RowParams row_params(const SampleKArgs& a, const RowRaw& raw, int rule_cap) {
   RowParams r;
-  r.T = raw.T;
-  r.top_p = raw.top_p;
-  r.min_p = raw.min_p;
   r.top_k = raw.top_k;
+  r.theta = (float)(1.0 - raw.top_p);
+  r.cmin = a.min_p_rows ? (float)log(raw.min_p) : a.min_p_log;
+  r.invT = (float)(1.0 / raw.T);
+  r.rTc = 1.0 / (double)(float)fmax(raw.T, 1e-5);
+  r.tscale = raw.T != 1.0;
   r.use_k = r.top_k > 0 && r.top_k < a.V;
-  r.use_p = r.top_p > 0.0f && r.top_p < 1.0f;
-  r.use_m = r.min_p != 0.0f;
-  r.greedy = !(r.T > 0.0f);
+  r.use_p = raw.top_p > 0.0 && raw.top_p < 1.0;
+  r.use_m = raw.min_p != 0.0;
+  r.greedy = !(raw.T > 0.0);
   const bool bk = r.use_k && r.top_k <= rule_cap;
   r.tk = r.tm = r.tp = false;
   if (!r.greedy) {
@@ -184,9 +195,6 @@ __device__ __forceinline__ RowParams row_params(const SampleKArgs& a, const RowR
   return r;
 }
 
-__device__ __forceinline__ float min_p_log(const SampleKArgs& a, float min_p) {
-  return a.min_p_rows ? (float)log((double)min_p) : a.min_p_log;
-}
 
 // Element e of a 16-byte group (DT 0: 4 x float32, DT 1: 8 x bfloat16).
 __device__ __forceinline__ uint32_t comp(const uint4& v, int i) {
@@ -381,6 +389,7 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
 template <int DT, int R>
 __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logits, const int32_t* __restrict__ hist,
                                                    long long row_stride, int G, int SL, int V, int hs, int pen,
+                                                   int hshare,
                                                    SampleKArgs a, FastPlan P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ SliceSmem sm;
@@ -409,7 +418,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logi
   // Every vector load is unconditional, from a clamped in-bounds address, so
   // the number of loads in flight is the same on every path and each wait is
   // for exactly the loads it needs.
-  const int32_t* hrow = hist + (long long)b * hs;
+  const int32_t* hrow = hist + (long long)(b / hshare) * hs;
   if (pen) {
     if (pf) {
       // the addresses do not need the length, which is read after the
@@ -633,7 +642,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logi
 
   // 4. candidate threshold
   float tau = -INFINITY;
-  if (rp.tm) tau = ms + min_p_log(a, rp.min_p);
+  if (rp.tm) tau = ms + rp.cmin;
   if (rp.tk || rp.tp) {
     const float tl = ladder_tau<R>(gm, patch, npatch, ms, rp.tk ? rp.top_k : 0, P.cap, sm);
     tau = rp.tm ? fmaxf(tau, tl) : tl;
@@ -1097,7 +1106,7 @@ struct BlockStore {
 // the top-p cut is not settled by [Zlo, Zhi] (the row goes to the exact engine).
 template <typename St>
 __device__ __forceinline__ bool run_filters(St& st, const SampleKArgs& a, const RowParams& rp, float m, float tcov, ZBounds zb) {
-  const float theta = (float)(1.0 - (double)rp.top_p);
+  const float theta = rp.theta;
   bool none = false;
   // Top-p keeps i iff S - head_excl(i) > floor(theta Z).  With Z only known
   // to lie in [Zlo, Zhi] the cut is taken when both ends agree.  S is the
@@ -1130,7 +1139,7 @@ __device__ __forceinline__ bool run_filters(St& st, const SampleKArgs& a, const 
     if (Rhi > Scov) return false;
     return st.keep_pcut((uint64_t)Rlo, (uint64_t)Rhi, tcov);
   };
-  const float thr = m + min_p_log(a, rp.min_p);
+  const float thr = m + rp.cmin;
   if (a.chain == WH_CHAIN_MLX && rp.use_k && rp.use_p) {
     // k -> p -> min-p; the candidates hold the whole top-k set
     st.topk_filter(rp.top_k);
@@ -1298,7 +1307,7 @@ __device__ __forceinline__ void totals4(const uint64_t (*acc)[64], uint64_t (&t)
 __device__ __forceinline__ int quick_filters(const RowParams& rp, ZBounds zb, uint64_t m_cov) {
   if (!rp.use_p) return 0;
   if (zb.lo > zb.hi) return 3;
-  const float theta = (float)(1.0 - (double)rp.top_p);
+  const float theta = rp.theta;
   const long long Rlo = (long long)(zb.lo - floor_theta_z(theta, zb.lo));
   const long long Rhi = (long long)(zb.hi - floor_theta_z(theta, zb.hi));
   if (Rhi <= 0) return -1;
@@ -1323,7 +1332,7 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
                                           const HotList& hl, int N, uint64_t m_all, uint64_t m_cov, uint64_t ZV_all,
                                           ZBounds zb, MergeSmem& sm) {
   const int lane = threadIdx.x & 63;
-  const bool tscale = rp.T != 1.0f;
+  const bool tscale = rp.tscale;
   RegStore<NS> st;
   uint64_t wd[NS];
   st.al = 0;
@@ -1352,8 +1361,8 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
   if (!ok) return 3;
 
   // Draw: integer inverse CDF in vocabulary order over the kept slots.
-  const float invT = (float)(1.0 / (double)rp.T);
-  const double rTc = 1.0 / (double)(float)fmax((double)rp.T, 1e-5);
+  const float invT = rp.invT;
+  const double rTc = rp.rTc;
   uint64_t ZV;
   int tok = 0;
   if (all_kept) {
@@ -1432,8 +1441,8 @@ __device__ __noinline__ int merge_block(const SampleKArgs* ap, const FastPlan* p
   ZBounds zb{0ull, 0ull};
   if (rp.use_p) zb = z_bounds_loop(hd, G, m, st.mass(false, 0.0f));
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
-  const float invT = (float)(1.0 / (double)rp.T);
-  const double rTc = 1.0 / (double)(float)fmax((double)rp.T, 1e-5);
+  const float invT = rp.invT;
+  const double rTc = rp.rTc;
   const Pred pr = st.pr;
   const CandSource src = st.src;
   auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, rTc)); };
@@ -1527,10 +1536,10 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
     // bucket of its id; wave 0 scans both.
     const HotList hl = hot_list(dyn);
     const bool split = rp.use_m && !(a.chain == WH_CHAIN_MLX && rp.use_k && rp.use_p);
-    const float thr = split ? m + min_p_log(a, rp.min_p) : -INFINITY;
-    const bool tscale = rp.T != 1.0f;
-    const float invT = (float)(1.0 / (double)rp.T);
-    const double rTc = 1.0 / (double)(float)fmax((double)rp.T, 1e-5);
+    const float thr = split ? m + rp.cmin : -INFINITY;
+    const bool tscale = rp.tscale;
+    const float invT = rp.invT;
+    const double rTc = rp.rTc;
     const int hn = lane < G ? hd.n : 0;
     uint64_t mv[3] = {0ull, 0ull, 0ull};  // hot mass, covered hot mass, cold mass
     uint64_t e[QW], bh[QW];
@@ -1663,7 +1672,10 @@ static HostPlan make_plan(int B, int V, int dtype, int hcap) {
   for (;; ++g) {
     int sl = (V + g - 1) / g;
     sl = (sl + p.ept - 1) / p.ept * p.ept;
-    p.G = g;
+    // rounding the slice length up can leave trailing slices empty (bf16
+    // V = 40 over 4 slices of 16); drop them, so every slice starts inside
+    // the row and its clamped load addresses stay in bounds
+    p.G = (V + sl - 1) / sl;
     p.SL = sl;
     p.codes_bytes = hcap > 0 ? (sl * esz + 15) / 16 * 16 : 0;
     p.pcap = hcap > 0 ? std::min(hcap / 2, sl) : 0;
@@ -1713,7 +1725,7 @@ static int launch_slice_t(const SampleKArgs& k, const FastPlan& fp, size_t lds, 
   int rc = set_lds((const void*)fn, lds);
   if (rc) return rc;
   hipLaunchKernelGGL(fn, dim3(fp.G, k.B), dim3(FT), lds, st, (const char*)k.logits, k.hist, (long long)k.row_stride, fp.G,
-                     fp.SL, k.V, (int)k.hist_stride, k.hcap > 0 ? 1 : 0, k, fp);
+                     fp.SL, k.V, (int)k.hist_stride, k.hcap > 0 ? 1 : 0, k.hshare, k, fp);
   return WH_OK;
 }
 

@@ -20,13 +20,14 @@ struct SampleKArgs {
   const int32_t* hist;
   long long hist_stride;
   const int32_t* hist_len;
+  int hshare;  // logits rows per history row (>= 1)
   const float* u;
-  float T, top_p, min_p;
+  double T, top_p, min_p;
   int top_k;
   float min_p_log;  // fl32(ln(min_p)) computed on the host for the scalar min_p
-  const float* T_rows;
-  const float* top_p_rows;
-  const float* min_p_rows;
+  const double* T_rows;
+  const double* top_p_rows;
+  const double* min_p_rows;
   const int32_t* top_k_rows;
   float rep, pres, freq;
   int rep_ctx, pres_ctx, freq_ctx;

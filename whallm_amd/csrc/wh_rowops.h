@@ -97,7 +97,7 @@ __device__ void build_penalties(const SampleKArgs& a, int b, RowCtx& rc, char* d
   const int wp = on_p ? window(a.pres_ctx) : 0;
   const int wf = on_f ? window(a.freq_ctx) : 0;
   const int W = max(wr, max(wp, wf));
-  const int32_t* h = a.hist + (long long)b * a.hist_stride;
+  const int32_t* h = a.hist + (long long)(b / a.hshare) * a.hist_stride;
   for (int j = len - W + tid; j < len; j += nt) {
     int t = h[j];
     if (t < lo || t >= hi || t >= a.V) continue;
@@ -403,13 +403,15 @@ __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_sm
   rc.hmask = -1;
   if (a.hcap > 0) build_penalties(a, b, rc, dyn_smem, 0, V);
 
-  const float T = a.T_rows ? a.T_rows[b] : a.T;
-  const float top_p = a.top_p_rows ? a.top_p_rows[b] : a.top_p;
-  const float min_p = a.min_p_rows ? a.min_p_rows[b] : a.min_p;
+  // the caller's doubles; the float32 constants below are derived from them
+  // as MLX derives them from Python floats
+  const double T = a.T_rows ? a.T_rows[b] : a.T;
+  const double top_p = a.top_p_rows ? a.top_p_rows[b] : a.top_p;
+  const double min_p = a.min_p_rows ? a.min_p_rows[b] : a.min_p;
   const int top_k = a.top_k_rows ? a.top_k_rows[b] : a.top_k;
   float* out = a.out_rows ? a.out_rows + (long long)b * V : nullptr;
 
-  if (!(T > 0.0f)) {
+  if (!(T > 0.0)) {
     // greedy: lowest index among the maxima (mx.argmax)
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
@@ -433,9 +435,9 @@ __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_sm
   const float m = block_reduce(lmax, sm.scratchf, OpMaxF(), -INFINITY);
 
   const bool use_k = top_k > 0 && top_k < V;
-  const bool use_p = top_p > 0.0f && top_p < 1.0f;
-  const bool use_m = min_p != 0.0f;
-  const float theta = (float)(1.0 - (double)top_p);
+  const bool use_p = top_p > 0.0 && top_p < 1.0;
+  const bool use_m = min_p != 0.0;
+  const float theta = (float)(1.0 - top_p);
   Pred pr = {0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
   auto mass = [m](int, float l) { return exp_fix44(l - m); };
   auto one = [](int, float) { return (uint64_t)1; };
@@ -469,7 +471,7 @@ __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_sm
     pr.cp = cp;
   };
   auto apply_m = [&]() {
-    const float c = a.min_p_rows ? (float)log((double)min_p) : a.min_p_log;
+    const float c = a.min_p_rows ? (float)log(min_p) : a.min_p_log;
     pr.use_m = 1;
     pr.thr = m + c;
   };
@@ -496,8 +498,8 @@ __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_sm
   }
 
   // Draw: per-thread contiguous segments, integer inverse CDF in vocab order.
-  const float invT = (float)(1.0 / (double)T);
-  const double rTc = 1.0 / (double)(float)fmax((double)T, 1e-5);
+  const float invT = (float)(1.0 / T);
+  const double rTc = 1.0 / (double)(float)fmax(T, 1e-5);
   const int seg = (V + nt - 1) / nt;
   const int lo = min(V, tid * seg), hi = min(V, lo + seg);
   uint64_t s = 0;

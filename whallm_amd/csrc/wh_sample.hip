@@ -87,13 +87,14 @@ int wh::prepare_sample(const wh_sample_args* p, SampleKArgs* k, bool need_draw) 
   if (p->row_stride < p->V) return fail(WH_EINVAL, "row_stride (%lld) < V (%d)", (long long)p->row_stride, p->V);
   if (!p->logits && p->B > 0) return fail(WH_EINVAL, "logits is NULL");
   if (p->chain != WH_CHAIN_MLX && p->chain != WH_CHAIN_WHALLM) return fail(WH_EINVAL, "chain must be WH_CHAIN_MLX or WH_CHAIN_WHALLM");
-  if (!p->temperature_rows && !(p->temperature >= 0.0f)) return fail(WH_EINVAL, "temperature must be >= 0");
-  if (!p->min_p_rows && !(p->min_p >= 0.0f && p->min_p <= 1.0f))
+  if (!p->temperature_rows && !(p->temperature >= 0.0)) return fail(WH_EINVAL, "temperature must be >= 0");
+  if (!p->min_p_rows && !(p->min_p >= 0.0 && p->min_p <= 1.0))
     return fail(WH_EINVAL, "`min_p` has to be a float in the [0, 1] interval, but is %g", (double)p->min_p);
   if (!p->top_k_rows && p->top_k < 0) return fail(WH_EINVAL, "top_k must be >= 0");
-  if (p->chain == WH_CHAIN_MLX && !p->top_k_rows && !p->temperature_rows && p->temperature > 0.0f && p->top_k > 0 &&
+  if (p->chain == WH_CHAIN_MLX && !p->top_k_rows && !p->temperature_rows && p->temperature > 0.0 && p->top_k > 0 &&
       p->top_k >= p->V)
     return fail(WH_EINVAL, "`top_k` has to be an integer in the (0, %d] interval, but is %d.", p->V, p->top_k);
+  if (p->history_share < 0) return fail(WH_EINVAL, "history_share must be >= 0");
   if (p->repetition_penalty < 0.0f) return fail(WH_EINVAL, "penalty must be a non-negative float, got %g", (double)p->repetition_penalty);
   if (need_draw && p->tokens && !p->uniforms && p->B > 0) return fail(WH_EINVAL, "uniforms is NULL but tokens were requested");
   if (p->out_mode != WH_OUT_LOGPROBS && p->out_mode != WH_OUT_MASKED) return fail(WH_EINVAL, "out_mode must be WH_OUT_LOGPROBS or WH_OUT_MASKED");
@@ -109,11 +110,12 @@ int wh::prepare_sample(const wh_sample_args* p, SampleKArgs* k, bool need_draw) 
   k->hist = p->history;
   k->hist_stride = p->history_stride;
   k->hist_len = p->history_len;
+  k->hshare = p->history_share > 1 ? p->history_share : 1;
   k->u = p->uniforms;
   k->T = p->temperature;
   k->top_p = p->top_p;
   k->min_p = p->min_p;
-  k->min_p_log = (float)log((double)p->min_p);
+  k->min_p_log = (float)log(p->min_p);
   k->top_k = p->top_k;
   k->T_rows = p->temperature_rows;
   k->top_p_rows = p->top_p_rows;

@@ -128,8 +128,8 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
     L.require_device(logits)
     B, V = logits.shape
     dev = logits.device
-    rows = (_rows_param(temperature_rows, B, torch.float32, dev), _rows_param(top_p_rows, B, torch.float32, dev),
-            _rows_param(min_p_rows, B, torch.float32, dev), _rows_param(top_k_rows, B, torch.int32, dev))
+    rows = (_rows_param(temperature_rows, B, torch.float64, dev), _rows_param(top_p_rows, B, torch.float64, dev),
+            _rows_param(min_p_rows, B, torch.float64, dev), _rows_param(top_k_rows, B, torch.int32, dev))
     if uniforms is None:
         uniforms = torch.rand(B, device=dev, dtype=torch.float32, generator=generator)
     else:
@@ -161,15 +161,32 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
     return tokens if len(res) == 1 else tuple(res)
 
 
+def _bound(name, t, dtype, shape):
+    """A buffer a pre-bound call reads on every invocation: it must already be
+    exactly what the kernel reads, or later refills by the caller would not
+    reach the kernel (a converted copy would be read instead)."""
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor) or t.dtype != dtype or tuple(t.shape) != tuple(shape) or not t.is_contiguous():
+        got = f"{t.dtype} {tuple(t.shape)}" if isinstance(t, torch.Tensor) else type(t).__name__
+        raise ValueError(f"{name} must be a contiguous {dtype} tensor of shape {tuple(shape)} (got {got}): "
+                         "a pre-bound call reads the caller's buffer itself on every call")
+    return t
+
+
 class SampleCall:
     """A wh_sample launch bound to fixed device buffers.
 
     For decode loops that refill the same logits / history / uniform buffers
     every step: the C argument struct is built once, and each call is one
     ctypes call into wh_sample on the stream current at construction.  Takes
-    the keyword arguments of sample(); `uniforms` is required (a buffer the
-    caller refills) and the outputs are the attributes `tokens` (and `kept`
-    with return_kept).
+    the keyword arguments of sample(); `uniforms` is required.  Every buffer
+    must already be in the layout the kernel reads -- logits float32 or
+    bfloat16 [B, V] with unit last stride, history int32 [B, H], history_len
+    int32 [B], uniforms float32 [B], per-row parameters float64 / int32 [B] --
+    because the call keeps reading the caller's buffers (a ValueError names
+    the first that is not).  The outputs are the attributes `tokens` (and
+    `kept` with return_kept).
     """
 
     def __init__(self, logits: torch.Tensor, *, uniforms: torch.Tensor, temperature: float = 0.0,
@@ -178,21 +195,33 @@ class SampleCall:
                  frequency_penalty: float = 0.0, repetition_context: int = 20, presence_context: int = 20,
                  frequency_context: int = 20, temperature_rows=None, top_p_rows=None, min_p_rows=None,
                  top_k_rows=None, return_kept: bool = False, engine: str = "auto"):
-        logits, dt = _as_rows(logits)
+        if not isinstance(logits, torch.Tensor) or logits.dim() != 2 or logits.stride(1) != 1 or \
+                logits.dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("logits must be a float32 or bfloat16 [B, V] tensor with unit last stride")
+        dt = L.DTYPE_F32 if logits.dtype == torch.float32 else L.DTYPE_BF16
         L.require_device(logits)
         B, V = logits.shape
         dev = logits.device
-        rows = (_rows_param(temperature_rows, B, torch.float32, dev), _rows_param(top_p_rows, B, torch.float32, dev),
-                _rows_param(min_p_rows, B, torch.float32, dev), _rows_param(top_k_rows, B, torch.int32, dev))
-        u = torch.as_tensor(uniforms, dtype=torch.float32, device=dev).reshape(B)
-        if not u.is_contiguous():
-            raise ValueError("uniforms must be a contiguous [B] float32 buffer")
+        rows = (_bound("temperature_rows", temperature_rows, torch.float64, (B,)),
+                _bound("top_p_rows", top_p_rows, torch.float64, (B,)),
+                _bound("min_p_rows", min_p_rows, torch.float64, (B,)),
+                _bound("top_k_rows", top_k_rows, torch.int32, (B,)))
+        u = _bound("uniforms", uniforms, torch.float32, (B,))
+        if history is not None:
+            _bound("history", history, torch.int32, (B, history.shape[-1] if isinstance(history, torch.Tensor) else -1))
+            _bound("history_len", history_len, torch.int32, (B,))
+            if history_len is None:
+                raise ValueError("history_len must be given with history in a pre-bound call")
+        L.require_device(u, history, history_len, *rows)
         self.tokens = torch.empty(B, dtype=torch.int32, device=dev)
         self.kept = torch.empty(B, dtype=torch.int32, device=dev) if return_kept else None
         self.args = L.SampleArgs()
         keep = _fill_args(self.args, logits, dt, chain, history, history_len, temperature, top_p, top_k, min_p,
                           repetition_penalty, presence_penalty, frequency_penalty, repetition_context,
                           presence_context, frequency_context, rows)
+        if history is not None and (keep[0].data_ptr() != history.data_ptr() or
+                                    keep[1].data_ptr() != history_len.data_ptr()):
+            raise ValueError("history buffers were copied: pass int32 [B, H] history and int32 [B] history_len")
         self.args.uniforms = u.data_ptr()
         self.args.tokens = self.tokens.data_ptr()
         self.args.kept_count = L.ptr(self.kept)
@@ -337,25 +366,24 @@ def verify_fused(target_logits: torch.Tensor, draft_probs: torch.Tensor, draft_t
 
 class VerifyCall:
     """A wh_verify_fused launch bound to fixed device buffers (target logits
-    [B, n+1, V], draft probabilities [B, n, V], draft tokens [B, n],
-    uniforms [B, n+1]); each call is one ctypes call on the stream current at
-    construction.  Outputs are the attributes `accepted` and `token`."""
+    float32 [B, n+1, V], draft probabilities float32 [B, n, V], draft tokens
+    int32 [B, n], uniforms float32 [B, n+1], all contiguous: the call keeps
+    reading the caller's buffers, so a buffer in any other layout raises
+    ValueError instead of being copied).  Each call is one ctypes call on the
+    stream current at construction; outputs are the attributes `accepted`
+    and `token`."""
 
     def __init__(self, target_logits: torch.Tensor, draft_probs: torch.Tensor, draft_tokens: torch.Tensor,
                  temperature: float, uniforms: torch.Tensor):
-        target = target_logits
-        if target.dtype != torch.float32 or not target.is_contiguous():
-            raise ValueError("target logits must be a contiguous float32 [B, n+1, V] buffer")
-        B, n1, V = target.shape
+        if not isinstance(target_logits, torch.Tensor) or target_logits.dim() != 3:
+            raise ValueError("target logits must be a float32 [B, n+1, V] tensor")
+        B, n1, V = target_logits.shape
         n = n1 - 1
-        dev = target.device
-        q = draft_probs if n > 0 else None
-        if q is not None and (q.dtype != torch.float32 or not q.is_contiguous() or tuple(q.shape) != (B, n, V)):
-            raise ValueError("draft probabilities must be a contiguous float32 [B, n, V] buffer")
-        toks = torch.as_tensor(draft_tokens, dtype=torch.int32, device=dev).reshape(B, n)
-        u = torch.as_tensor(uniforms, dtype=torch.float32, device=dev).reshape(B, n1)
-        if not toks.is_contiguous() or not u.is_contiguous():
-            raise ValueError("draft tokens and uniforms must be contiguous buffers")
+        dev = target_logits.device
+        target = _bound("target logits", target_logits, torch.float32, (B, n1, V))
+        q = _bound("draft probabilities", draft_probs, torch.float32, (B, n, V)) if n > 0 else None
+        toks = _bound("draft tokens", draft_tokens, torch.int32, (B, n))
+        u = _bound("uniforms", uniforms, torch.float32, (B, n1))
         L.require_device(target, q, toks, u)
         self.accepted = torch.empty(B, dtype=torch.int32, device=dev)
         self.token = torch.empty(B, dtype=torch.int32, device=dev)
