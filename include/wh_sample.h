@@ -125,6 +125,21 @@ typedef struct wh_sample_args {
 size_t wh_sample_workspace_bytes(int32_t B, int32_t V);
 int wh_sample(const wh_sample_args* args, void* stream);
 
+/* wh_sample without a workspace and without any allocation.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The fast engine's scratch (slice headers and candidates) is a
+ * library-owned device array of WH_NOALLOC_SCRATCH_BYTES on each GPU the
+ * library runs on, resolved on the first call on that GPU and held until the
+ * process ends; args->workspace and workspace_bytes are ignored.  Calls whose
+ * wh_sample_workspace_bytes(B, V) exceeds the array are rejected with
+ * WH_ELIMIT.  Every call on one GPU shares the array: calls that overlap on
+ * one GPU (two streams, two threads) race, as two calls on one workspace do.
+ * The stream's device must be the current device.  Results are those of
+ * wh_sample. */
+#define WH_NOALLOC_SCRATCH_BYTES (32u << 20)
+int wh_sample_noalloc(const wh_sample_args* args, void* stream);
+
 /* Penalty processors only, in place on float32 or bf16 logits (bf16 results
  * are rounded to nearest even).  Uses the history/penalty fields of args. */
 int wh_apply_penalties(const wh_sample_args* args, void* stream);

@@ -127,3 +127,13 @@ def test_python_mirror_validation_without_gpu():
     procs = su.make_logits_processors(repetition_penalty=1.1, presence_penalty=0.5, frequency_penalty=0.2)
     assert [p.kind for p in procs] == ["repetition", "presence", "frequency"]
     assert su.make_logits_processors() == []
+
+
+def test_noalloc_limit_is_checked_before_any_gpu_call(L):
+    # 4096 rows of V = 151,936 need far more than the no-allocation
+    # entry point's scratch: rejected with WH_ELIMIT before any HIP call
+    a = _args(L, B=4096, V=151936, row_stride=151936, uniforms=1 << 20, tokens=1 << 20)
+    assert L.lib().wh_sample_noalloc(ctypes.byref(a), None) == L.WH_ELIMIT
+    assert "WH_NOALLOC_SCRATCH_BYTES" in L.lib().wh_last_error().decode()
+    assert L.lib().wh_sample_workspace_bytes(4096, 151936) > L.NOALLOC_SCRATCH_BYTES
+    assert L.lib().wh_sample_workspace_bytes(64, 151936) <= L.NOALLOC_SCRATCH_BYTES

@@ -27,6 +27,7 @@ OUT_LOGPROBS = 0
 OUT_MASKED = 1
 MAX_VOCAB = 262144
 MAX_WINDOW = 4096
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -75,6 +76,8 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(LIB_PATH)
         L.wh_sample.argtypes = [ctypes.POINTER(SampleArgs), _p]
         L.wh_sample.restype = ctypes.c_int
+        L.wh_sample_noalloc.argtypes = [ctypes.POINTER(SampleArgs), _p]
+        L.wh_sample_noalloc.restype = ctypes.c_int
         L.wh_apply_penalties.argtypes = [ctypes.POINTER(SampleArgs), _p]
         L.wh_apply_penalties.restype = ctypes.c_int
         L.wh_sample_workspace_bytes.argtypes = [_i32, _i32]

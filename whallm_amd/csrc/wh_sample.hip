@@ -15,6 +15,8 @@
 // probability mass for top-p -- and the draw is an inverse CDF over integer
 // weights in vocabulary order, so results are bit-identical to the CPU
 // oracle whatever the reduction order.
+#include <mutex>
+
 #include "wh_rowops.h"
 
 namespace wh {
@@ -179,6 +181,55 @@ int wh::launch_sample_exact(const SampleKArgs& k, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "sample_exact_kernel launch failed: %s", hipGetErrorString(e));
   return WH_OK;
+}
+
+// The no-allocation entry point's scratch: a file-scope device array (zero
+// initialised in the code object, so it adds nothing to the file), one copy
+// per GPU at its own address.  Host code never passes `scratch` itself -- its
+// host-side name is not a device address -- only the address
+// hipGetSymbolAddress returns for the current device, cached per device.
+static __device__ __align__(256) char scratch[WH_NOALLOC_SCRATCH_BYTES];
+
+constexpr int WH_SCRATCH_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[WH_SCRATCH_DEVICES];
+
+static int scratch_for_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(WH_EHIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= WH_SCRATCH_DEVICES) return fail(WH_ELIMIT, "device %d beyond the %d the scratch table holds", dev, WH_SCRATCH_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(WH_EHIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return WH_OK;
+}
+
+extern "C" int wh_sample_noalloc(const wh_sample_args* args, void* stream) {
+  clear_error();
+  SampleKArgs k;
+  int rc = prepare_sample(args, &k, true);
+  if (rc) return rc;
+  if (!args->tokens && !args->logprobs_out && !args->kept_count) return WH_OK;
+  if (k.B == 0) return WH_OK;
+  const size_t need = wh::sample_workspace_bytes(k.B, k.V);
+  if (need > WH_NOALLOC_SCRATCH_BYTES)
+    return fail(WH_ELIMIT,
+                "wh_sample_noalloc: %d rows of V=%d need %zu bytes of scratch, beyond its maximum of %u bytes "
+                "(WH_NOALLOC_SCRATCH_BYTES); call wh_sample with a workspace instead",
+                k.B, k.V, need, (unsigned)WH_NOALLOC_SCRATCH_BYTES);
+  void* ptr = nullptr;
+  rc = scratch_for_current_device(&ptr);
+  if (rc) return rc;
+  wh_sample_args a = *args;
+  a.workspace = ptr;
+  a.workspace_bytes = WH_NOALLOC_SCRATCH_BYTES;
+  return wh::launch_sample(k, &a, (hipStream_t)stream);
 }
 
 extern "C" int wh_apply_penalties(const wh_sample_args* args, void* stream) {

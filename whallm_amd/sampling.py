@@ -122,7 +122,9 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
     Returns int32 tokens [B]; with return_logprobs (chain "whallm" only) also
     the sampling_logprobs rows [B, V]; with return_kept the kept-set sizes.
     engine "exact" forces the multi-pass engine (no workspace) -- both
-    engines return identical results; "auto" picks the sliced single-read one.
+    engines return identical results; "auto" picks the sliced single-read one;
+    "noalloc" calls wh_sample_noalloc, which uses the library's own device
+    scratch instead of a workspace (same results, no allocation).
     """
     logits, dt = _as_rows(logits)
     L.require_device(logits)
@@ -146,12 +148,15 @@ def sample(logits: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0
     a.kept_count = L.ptr(kept)
     a.logprobs_out = L.ptr(out)
     a.out_mode = L.OUT_LOGPROBS
-    if engine != "exact":
+    fn = L.lib().wh_sample
+    if engine == "noalloc":
+        fn = L.lib().wh_sample_noalloc
+    elif engine != "exact":
         nb = L.lib().wh_sample_workspace_bytes(B, V)
         ws = L.workspace(dev, nb)
         a.workspace = ws.data_ptr()
         a.workspace_bytes = ws.numel()
-    L.check(L.lib().wh_sample(ctypes.byref(a), ctypes.c_void_p(L.stream_of(logits))))
+    L.check(fn(ctypes.byref(a), ctypes.c_void_p(L.stream_of(logits))))
     del keep
     res = [tokens]
     if return_logprobs:
