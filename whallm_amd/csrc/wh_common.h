@@ -121,6 +121,19 @@ __device__ __forceinline__ uint64_t comp_p(uint32_t key, int id) {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
+// max(a, b, c) as one v_max3_f32, for reductions over loaded logits.
+// Written as fmaxf, IEEE mode makes the compiler quiet every operand first
+// (one extra v_max_f32 x, x, x each) because bits loaded from memory could
+// be signalling NaNs, and keeps the two-operand form.  Logits are never
+// signalling NaNs here; the penalty marks are quiet NaNs, which the
+// instruction ignores (returning the max of the other operands) exactly as
+// fmaxf does.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // --------------------------------------------------------------------------
 // Wave / block reductions (blockDim.x a multiple of 64, <= 1024).
 // --------------------------------------------------------------------------
@@ -194,8 +207,9 @@ __device__ __forceinline__ uint64_t wsum_u64(uint64_t v) {
   return dpp_reduce_u64(v, [](uint64_t a, uint64_t b) { return a + b; });
 }
 __device__ __forceinline__ float wmax_f(float v) {
-  return __uint_as_float(
-      dpp_reduce_u32(__float_as_uint(v), [](uint32_t a, uint32_t b) { return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b))); }));
+  return __uint_as_float(dpp_reduce_u32(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(max3_raw(__uint_as_float(a), __uint_as_float(b), __uint_as_float(b)));
+  }));
 }
 __device__ __forceinline__ int wmin_i(int v) {
   return (int)dpp_reduce_u32((uint32_t)v, [](uint32_t a, uint32_t b) { return (uint32_t)min((int)a, (int)b); });

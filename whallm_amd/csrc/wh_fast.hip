@@ -213,13 +213,14 @@ __device__ __forceinline__ float elem_n(const uint4& v, int e) {
 }
 template <int DT>
 __device__ __forceinline__ float grp_max(const uint4& v) {
-  if (DT == 0)
-    return fmaxf(fmaxf(__uint_as_float(v.x), __uint_as_float(v.y)), fmaxf(__uint_as_float(v.z), __uint_as_float(v.w)));
-  const float a = fmaxf(fmaxf(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u)),
-                        fmaxf(__uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u)));
-  const float c = fmaxf(fmaxf(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u)),
-                        fmaxf(__uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u)));
-  return fmaxf(a, c);
+  if (DT == 0) {
+    const float a = max3_raw(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z));
+    return max3_raw(a, __uint_as_float(v.w), __uint_as_float(v.w));
+  }
+  float m = max3_raw(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u), __uint_as_float(v.y << 16));
+  m = max3_raw(m, __uint_as_float(v.y & 0xFFFF0000u), __uint_as_float(v.z << 16));
+  m = max3_raw(m, __uint_as_float(v.z & 0xFFFF0000u), __uint_as_float(v.w << 16));
+  return max3_raw(m, __uint_as_float(v.w & 0xFFFF0000u), __uint_as_float(v.w & 0xFFFF0000u));
 }
 // Penalty code bits: count in the frequency window (bits 0-12, at most 4096),
 // in the repetition window (bit 13), in the presence window (bit 14).  A flag
@@ -572,7 +573,7 @@ __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logi
     const int g = v0 + (r * FT + tid) * EPT;
     if (g >= v1) d[r] = make_uint4(NEG, NEG, NEG, NEG);
     gm[r] = grp_max<DT>(d[r]);
-    mx = fmaxf(mx, gm[r]);
+    mx = max3_raw(mx, gm[r], gm[r]);
   }
   if (pen) {
 #pragma unroll
@@ -587,16 +588,17 @@ __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logi
       const float v = pc.apply(__uint_as_float(raw) + 0.0f, ocode[q]);
       const int slot = atomicAdd(&sm.npatch, 1);
       if (slot < P.pcap) patch[slot] = make_int2(__float_as_int(v), t);
-      pmax = fmaxf(pmax, v);
+      pmax = max3_raw(pmax, v, v);
     }
   }
-  mx = fmaxf(mx, pmax);
+  mx = max3_raw(mx, pmax, pmax);
   mx = wmax_f(mx);
   if (lane == 0) sm.redm[wv] = mx;
   __syncthreads();
   float ms = sm.redm[0];
 #pragma unroll
-  for (int w = 1; w < FNW; ++w) ms = fmaxf(ms, sm.redm[w]);
+  for (int w = 1; w + 1 < FNW; w += 2) ms = max3_raw(ms, sm.redm[w], sm.redm[w + 1]);
+  if (FNW % 2 == 0) ms = max3_raw(ms, sm.redm[FNW - 1], sm.redm[FNW - 1]);
   const int npatch_raw = sm.npatch;
   const int npatch = min(npatch_raw, P.pcap);
 
