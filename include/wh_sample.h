@@ -26,6 +26,11 @@
  *                           sampling_logprobs(logits, T, top_p=1)
  *                           (dspark.py:663-670): target logits in, draft
  *                           probabilities q in.
+ *   wh_markov_logits        one DSpark draft position's logits:
+ *                           base_logits[:, position] + markov_head(previous)
+ *                           (dspark.py:157-165, 319-324;
+ *                           deepseek_v41/dspark.py:131-133), with `previous`
+ *                           read from device memory.
  *
  * Random numbers: the reference draws from MLX's global PRNG
  * (mx.random.categorical / uniform, dspark.py:329, 884, 904).  This library
@@ -165,6 +170,34 @@ typedef struct wh_verify_args {
 size_t wh_verify_workspace_bytes(int32_t B, int32_t n, int32_t V);
 int wh_verify_logprobs(const wh_verify_args* args, void* stream);
 int wh_verify_fused(const wh_verify_args* args, void* stream);
+
+/* One DSpark draft position (dspark.py:319-324):
+ *   logits_out = base + markov_w2 @ float32(markov_w1[*prev])
+ * markov_w1 is the Markov head's embedding [V, rank] and markov_w2 its
+ * output projection's weight [V, rank] (nn.Linear(rank, V)), both float32 or
+ * bf16.  *prev is read on the device (clamped to [0, V)), so the previous
+ * position's wh_sample token feeds the next position with no host sync.  The
+ * float32 sum is formed in a fixed order (8-entry fused multiply-add chains,
+ * then a 32-way butterfly), which the CPU oracle reproduces bit for bit; the
+ * reference's order (an MLX matrix-vector product) is unspecified. */
+typedef struct wh_markov_args {
+  const float* base;         /* device, [V] float32: base_logits[0, position] */
+  const void* embed;         /* device, [V, rank] markov_w1 weight, 16-byte aligned */
+  const void* proj;          /* device, [V, rank] markov_w2 weight, 16-byte aligned */
+  int32_t dtype;             /* WH_DTYPE_F32 or WH_DTYPE_BF16 (both weights) */
+  int32_t V;
+  int32_t rank;              /* a multiple of 8, at most 256 */
+  int32_t reserved;
+  const int32_t* prev;       /* device, [1]: the previous token */
+  float* logits_out;         /* device, [V] float32 */
+} wh_markov_args;
+int wh_markov_logits(const wh_markov_args* args, void* stream);
+
+/* Test hook: with on != 0, every entry of wh_verify_fused's sliced form
+ * takes the exact per-row algorithm that entries the normaliser bounds leave
+ * undecided take (same results, slower).  Process wide; returns the previous
+ * setting. */
+int wh_verify_force_exact(int on);
 
 /* The contract exponential on device (floor(2^44 exp(d)) for d <= 0), for
  * bit-exactness tests against the CPU oracle. */

@@ -78,6 +78,10 @@ def lib():
         L.who_reject_fused_export.argtypes = [f32, f32, ctypes.c_uint64, ctypes.c_uint64]
         L.who_reject_lp_export.restype = i32
         L.who_reject_lp_export.argtypes = [f32, f32, f32]
+        L.who_markov_logits.restype = i32
+        L.who_markov_logits.argtypes = [P, P, P, i32, i32, i32, i32, P]
+        L.who_top_logprobs.restype = i32
+        L.who_top_logprobs.argtypes = [P, i32, i32, i64, i32, P, P]
         L.who_penalize_rows.restype = None
         L.who_penalize_rows.argtypes = [P, i32, i32, i64, P, i64, P, P]
         _lib = L
@@ -208,6 +212,36 @@ def verify_fused(target_logits, draft_q, draft_tok, u, temperature, threads=None
     if rc != 0:
         raise ValueError(f"oracle rejected the arguments (code {rc})")
     return acc, tok
+
+
+def markov_logits(base_row, w1, w2, prev: int):
+    """DSpark draft step logits: base_row + markov_w2 @ float32(markov_w1[prev])
+    in the contract's summation order (wh_oracle_ext.c).  w1, w2: [V, rank]
+    float32 arrays or bfloat16 bit patterns (uint16)."""
+    base_row = np.ascontiguousarray(base_row, dtype=np.float32)
+    dtype = 1 if w1.dtype == np.uint16 else 0
+    w1 = np.ascontiguousarray(w1)
+    w2 = np.ascontiguousarray(w2)
+    V, rank = w2.shape
+    out = np.empty(V, np.float32)
+    rc = lib().who_markov_logits(_ptr(base_row), _ptr(w1), _ptr(w2), dtype, V, rank, int(prev), _ptr(out))
+    if rc != 0:
+        raise ValueError("oracle rejected the Markov arguments")
+    return out
+
+
+def top_logprobs(logits, n: int):
+    """Top-n (ids, logprobs) per row: (value desc, id asc), logprob in float64."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    if logits.ndim == 1:
+        logits = logits[None]
+    B, V = logits.shape
+    ids = np.empty((B, n), np.int32)
+    lps = np.empty((B, n), np.float32)
+    rc = lib().who_top_logprobs(_ptr(logits), B, V, V, int(n), _ptr(ids), _ptr(lps))
+    if rc != 0:
+        raise ValueError("oracle rejected the top-logprob arguments")
+    return ids, lps
 
 
 def gt_theta(A: int, theta: float, Z: int) -> bool:

@@ -349,9 +349,9 @@ def test_verify_fused_workload3_full_size(S, dev, oracle):
 @pytest.mark.gpu
 @pytest.mark.parametrize("force_exact", [False, True])
 @pytest.mark.parametrize("seed", range(12))
-def test_verify_fused_sliced(S, dev, oracle, seed, force_exact, monkeypatch):
+def test_verify_fused_sliced(S, dev, oracle, seed, force_exact):
     """The sliced verifier (T > 0, V % 4 == 0): bounds-decided ratio tests,
-    exact residual draw; with WH_VERIFY_FORCE_EXACT every entry takes the
+    exact residual draw; with wh_verify_force_exact every entry takes the
     exact per-row algorithm that undecided entries use.  Seeds 10 and 11 use
     long drafts (n = 17, 63: the most the sliced form takes)."""
     rng = np.random.default_rng(700 + seed)
@@ -380,12 +380,16 @@ def test_verify_fused_sliced(S, dev, oracle, seed, force_exact, monkeypatch):
     if seed % 5 == 0:
         toks[0, 0] = V  # out of range: rejected
     u = rng.random((B, n + 1), dtype=np.float32)
-    if force_exact:
-        monkeypatch.setenv("WH_VERIFY_FORCE_EXACT", "1")
+    from whallm_amd import _lib
+
+    _lib.lib().wh_verify_force_exact(1 if force_exact else 0)
     oa, ot = oracle.verify_fused(x, q, toks, u, T)
     announce(f"wh_verify_fused sliced seed={seed} B={B} n={n} V={V} T={T} force_exact={force_exact}")
-    a, t = S.verify_fused(torch.from_numpy(x).to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(toks).to(dev),
-                          T, uniforms=torch.from_numpy(u).to(dev))
+    try:
+        a, t = S.verify_fused(torch.from_numpy(x).to(dev), torch.from_numpy(q).to(dev),
+                              torch.from_numpy(toks).to(dev), T, uniforms=torch.from_numpy(u).to(dev))
+    finally:
+        _lib.lib().wh_verify_force_exact(0)
     assert np.array_equal(a.cpu().numpy(), oa)
     assert np.array_equal(t.cpu().numpy(), ot)
 

@@ -58,6 +58,13 @@ class VerifyArgs(ctypes.Structure):
     ]
 
 
+class MarkovArgs(ctypes.Structure):
+    _fields_ = [
+        ("base", _p), ("embed", _p), ("proj", _p), ("dtype", _i32), ("V", _i32), ("rank", _i32), ("reserved", _i32),
+        ("prev", _p), ("logits_out", _p),
+    ]
+
+
 class WhError(RuntimeError):
     pass
 
@@ -88,6 +95,10 @@ def lib() -> ctypes.CDLL:
         L.wh_verify_fused.restype = ctypes.c_int
         L.wh_verify_workspace_bytes.argtypes = [_i32, _i32, _i32]
         L.wh_verify_workspace_bytes.restype = ctypes.c_size_t
+        L.wh_markov_logits.argtypes = [ctypes.POINTER(MarkovArgs), _p]
+        L.wh_markov_logits.restype = ctypes.c_int
+        L.wh_verify_force_exact.argtypes = [ctypes.c_int]
+        L.wh_verify_force_exact.restype = ctypes.c_int
         L.wh_exp_fix44.argtypes = [_p, _p, _i64, _p]
         L.wh_exp_fix44.restype = ctypes.c_int
         L.wh_last_error.argtypes = []

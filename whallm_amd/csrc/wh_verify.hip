@@ -15,6 +15,7 @@
 //
 // All decisions are exact: masses are floor(2^44 exp(.)) integers, the
 // ratio test u*q*Z > W is evaluated in 128-bit integers.
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 
@@ -768,12 +769,16 @@ static VHostPlan vplan(int B, int n, int V) {
   return h;
 }
 
+// Test hook (wh_verify_force_exact): route every batch entry of the sliced
+// verifier through the exact per-row algorithm that entries undecided by the
+// bounds take.  Off unless a test sets it.
+static std::atomic<int> g_verify_force_exact{0};
+
+extern "C" int wh_verify_force_exact(int on) { return g_verify_force_exact.exchange(on ? 1 : 0); }
+
 static int launch_verify_sliced(const VerifyKArgs& k, const VHostPlan& h, char* ws, hipStream_t st) {
   VPlan P;
-  // WH_VERIFY_FORCE_EXACT=1 (tests only) routes every batch entry through the
-  // exact per-row algorithm that entries undecided by the bounds take
-  const char* fe = getenv("WH_VERIFY_FORCE_EXACT");
-  P.force_exact = (fe && fe[0] == '1') ? 1 : 0;
+  P.force_exact = g_verify_force_exact.load(std::memory_order_relaxed);
   P.G1 = h.G1;
   P.SL1 = h.SL1;
   P.G2 = h.G2;
