@@ -31,6 +31,12 @@
  *                           (dspark.py:157-165, 319-324;
  *                           deepseek_v41/dspark.py:131-133), with `previous`
  *                           read from device memory.
+ *   wh_top_logprobs         the n most likely entries of mlx_lm's per-step
+ *                           logprobs = logits - logsumexp(logits)
+ *                           (generation.py:1465-1475) and the chosen token's,
+ *                           for the OpenAI `logprobs` / `top_logprobs` fields
+ *                           that runtime/deepseek_v4_ssd/server.py:1110-1111
+ *                           rejects today.
  *
  * Random numbers: the reference draws from MLX's global PRNG
  * (mx.random.categorical / uniform, dspark.py:329, 884, 904).  This library
@@ -67,6 +73,7 @@ extern "C" {
 
 #define WH_MAX_VOCAB 262144      /* V <= 2^18 keeps fixed-point sums below 2^62 */
 #define WH_MAX_WINDOW 4096       /* penalty window entries per row */
+#define WH_MAX_TOP_LOGPROBS 64   /* n of wh_top_logprobs */
 
 typedef struct wh_sample_args {
   const void* logits;        /* device, B rows of V values (dtype), row stride in elements */
@@ -192,6 +199,31 @@ typedef struct wh_markov_args {
   float* logits_out;         /* device, [V] float32 */
 } wh_markov_args;
 int wh_markov_logits(const wh_markov_args* args, void* stream);
+
+/* Top-n logprobs of B logit rows: logprob = float32(double(l) - lse) with
+ * lse = logsumexp(row) in float64; the n entries in order of value
+ * descending, lower ids first among equal values; -inf entries rank last and
+ * a row of all -inf gives -inf logprobs.  Pass the row the caller's logprobs
+ * are defined on (mlx_lm: the logits after the logits processors, before
+ * temperature).  With `token`, token_logprob[b] is row b's logprob of
+ * token[b] (-inf for an id outside [0, V)).  Inputs must hold no NaN. */
+typedef struct wh_top_logprobs_args {
+  const void* logits;        /* device, B rows of V (row_stride apart) */
+  int32_t dtype;             /* WH_DTYPE_F32 or WH_DTYPE_BF16 */
+  int32_t B;
+  int32_t V;                 /* 1 .. WH_MAX_VOCAB */
+  int32_t n;                 /* 1 .. min(V, WH_MAX_TOP_LOGPROBS) */
+  int64_t row_stride;        /* elements, >= V */
+  const int32_t* token;      /* device, [B], nullable */
+  int32_t* top_ids;          /* device, [B, n] */
+  float* top_logprobs;       /* device, [B, n] */
+  float* token_logprob;      /* device, [B], nullable (needs token) */
+  void* workspace;           /* device, 16-byte aligned,
+                                wh_top_logprobs_workspace_bytes(B, V, n) bytes */
+  size_t workspace_bytes;
+} wh_top_logprobs_args;
+size_t wh_top_logprobs_workspace_bytes(int32_t B, int32_t V, int32_t n);
+int wh_top_logprobs(const wh_top_logprobs_args* args, void* stream);
 
 /* Test hook: with on != 0, every entry of wh_verify_fused's sliced form
  * takes the exact per-row algorithm that entries the normaliser bounds leave

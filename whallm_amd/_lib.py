@@ -26,6 +26,7 @@ CHAIN_WHALLM = 1
 OUT_LOGPROBS = 0
 OUT_MASKED = 1
 MAX_VOCAB = 262144
+MAX_TOP_LOGPROBS = 64
 MAX_WINDOW = 4096
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -65,6 +66,14 @@ class MarkovArgs(ctypes.Structure):
     ]
 
 
+class TopLogprobsArgs(ctypes.Structure):
+    _fields_ = [
+        ("logits", _p), ("dtype", _i32), ("B", _i32), ("V", _i32), ("n", _i32), ("row_stride", _i64),
+        ("token", _p), ("top_ids", _p), ("top_logprobs", _p), ("token_logprob", _p),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class WhError(RuntimeError):
     pass
 
@@ -97,6 +106,10 @@ def lib() -> ctypes.CDLL:
         L.wh_verify_workspace_bytes.restype = ctypes.c_size_t
         L.wh_markov_logits.argtypes = [ctypes.POINTER(MarkovArgs), _p]
         L.wh_markov_logits.restype = ctypes.c_int
+        L.wh_top_logprobs.argtypes = [ctypes.POINTER(TopLogprobsArgs), _p]
+        L.wh_top_logprobs.restype = ctypes.c_int
+        L.wh_top_logprobs_workspace_bytes.argtypes = [_i32, _i32, _i32]
+        L.wh_top_logprobs_workspace_bytes.restype = ctypes.c_size_t
         L.wh_verify_force_exact.argtypes = [ctypes.c_int]
         L.wh_verify_force_exact.restype = ctypes.c_int
         L.wh_exp_fix44.argtypes = [_p, _p, _i64, _p]
