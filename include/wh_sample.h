@@ -37,6 +37,11 @@
  *                           for the OpenAI `logprobs` / `top_logprobs` fields
  *                           that runtime/deepseek_v4_ssd/server.py:1110-1111
  *                           rejects today.
+ *   wh_history_append       the per-step history extension the logits
+ *                           processors read: mlx_lm generate_step's
+ *                           `tokens = concat([tokens, y])` and the MTP loop's
+ *                           sampling_tokens.append (qwen4_exp.py:1143-1149),
+ *                           on a device buffer.
  *
  * Random numbers: the reference draws from MLX's global PRNG
  * (mx.random.categorical / uniform, dspark.py:329, 884, 904).  This library
@@ -224,6 +229,29 @@ typedef struct wh_top_logprobs_args {
 } wh_top_logprobs_args;
 size_t wh_top_logprobs_workspace_bytes(int32_t B, int32_t V, int32_t n);
 int wh_top_logprobs(const wh_top_logprobs_args* args, void* stream);
+
+/* Append ids to B device-resident histories (the [B, capacity] buffer and
+ * lengths wh_sample reads as history / history_len).  Row b receives
+ * tokens[b, 0 .. counts[b]) (all m without counts), then tail[b] if tail is
+ * given -- the MTP commit: accepted drafts, then the verifier's next token.
+ * A row that would exceed capacity first keeps only its last `keep` ids,
+ * moved to the front; keep must cover every penalty context in use (a
+ * context of 0, the whole history, needs a capacity that never fills).
+ * Requires keep + m (+1 with tail) <= capacity.  Lengths outside
+ * [0, capacity] are clamped. */
+typedef struct wh_history_args {
+  int32_t* history;          /* device, [B, history_stride] */
+  int64_t history_stride;    /* elements, >= capacity */
+  int32_t* history_len;      /* device, [B], read and updated */
+  int32_t B;
+  int32_t capacity;
+  int32_t keep;              /* 0 .. WH_MAX_WINDOW */
+  int32_t m;                 /* ids per row in tokens */
+  const int32_t* tokens;     /* device, [B, m] */
+  const int32_t* counts;     /* device, [B], nullable: ids to take per row (clamped to [0, m]) */
+  const int32_t* tail;       /* device, [B], nullable */
+} wh_history_args;
+int wh_history_append(const wh_history_args* args, void* stream);
 
 /* Test hook: with on != 0, every entry of wh_verify_fused's sliced form
  * takes the exact per-row algorithm that entries the normaliser bounds leave

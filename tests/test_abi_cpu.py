@@ -45,7 +45,8 @@ def test_struct_layouts_match_ctypes(L, tmp_path):
     against the ctypes mirror."""
     lines = []
     for cname, cls in (("wh_sample_args", L.SampleArgs), ("wh_verify_args", L.VerifyArgs), ("wh_markov_args", L.MarkovArgs),
-                      ("wh_top_logprobs_args", L.TopLogprobsArgs)):
+                      ("wh_top_logprobs_args", L.TopLogprobsArgs),
+                      ("wh_history_args", L.HistoryArgs)):
         lines.append(f'printf("%zu\\n", sizeof({cname}));')
         for f in cls._fields_:
             lines.append(f'printf("%zu\\n", offsetof({cname}, {f[0]}));')
@@ -56,7 +57,7 @@ def test_struct_layouts_match_ctypes(L, tmp_path):
     subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(prog), "-o", str(exe)], check=True)
     got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()))
     want = []
-    for cls in (L.SampleArgs, L.VerifyArgs, L.MarkovArgs, L.TopLogprobsArgs):
+    for cls in (L.SampleArgs, L.VerifyArgs, L.MarkovArgs, L.TopLogprobsArgs, L.HistoryArgs):
         want.append(ctypes.sizeof(cls))
         want += [getattr(cls, f[0]).offset for f in cls._fields_]
     assert got == want
@@ -138,3 +139,44 @@ def test_noalloc_limit_is_checked_before_any_gpu_call(L):
     assert "WH_NOALLOC_SCRATCH_BYTES" in L.lib().wh_last_error().decode()
     assert L.lib().wh_sample_workspace_bytes(4096, 151936) > L.NOALLOC_SCRATCH_BYTES
     assert L.lib().wh_sample_workspace_bytes(64, 151936) <= L.NOALLOC_SCRATCH_BYTES
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(keep=20, m=10, capacity=25), "capacity"),
+    (dict(keep=5000, capacity=8192, history_stride=8192), "keep"),
+    (dict(history_stride=10), "history_stride"),
+    (dict(capacity=0), "capacity"),
+    (dict(m=-1), "m must"),
+])
+def test_history_append_validation(L, kw, needle):
+    a = L.HistoryArgs()
+    a.history, a.history_len, a.tokens = 1 << 20, 1 << 20, 1 << 20
+    a.B, a.capacity, a.history_stride, a.keep, a.m = 2, 64, 64, 20, 1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    rc = L.lib().wh_history_append(ctypes.byref(a), None)
+    assert rc in (L.WH_EINVAL, L.WH_ELIMIT)
+    assert needle in L.lib().wh_last_error().decode()
+
+
+def test_top_logprobs_validation(L):
+    a = L.TopLogprobsArgs()
+    a.logits, a.top_ids, a.top_logprobs = 1 << 20, 1 << 20, 1 << 20
+    a.B, a.V, a.n, a.row_stride = 2, 100, 65, 100
+    assert L.lib().wh_top_logprobs(ctypes.byref(a), None) == L.WH_ELIMIT
+    a.n = 5
+    assert L.lib().wh_top_logprobs(ctypes.byref(a), None) == L.WH_EINVAL  # no workspace
+    assert "workspace" in L.lib().wh_last_error().decode()
+    assert L.lib().wh_top_logprobs_workspace_bytes(2, 100, 5) == 2 * 16 + 2 * 5 * 8
+
+
+def test_decode_state_host_checks():
+    from whallm_amd.decode import DecodeState, TokenSelector
+
+    with pytest.raises(ValueError):
+        DecodeState(2, 20, 20, "cpu")
+    sel = TokenSelector(temperature=0.7, repetition_penalty=1.2, repetition_context=32, presence_penalty=0.5,
+                        presence_context=8)
+    assert sel.window == 32 and sel.penalised
+    assert TokenSelector(presence_penalty=0.5, presence_context=0).window is None
+    assert not TokenSelector(repetition_penalty=1.0).penalised

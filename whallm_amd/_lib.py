@@ -74,6 +74,13 @@ class TopLogprobsArgs(ctypes.Structure):
     ]
 
 
+class HistoryArgs(ctypes.Structure):
+    _fields_ = [
+        ("history", _p), ("history_stride", _i64), ("history_len", _p), ("B", _i32), ("capacity", _i32),
+        ("keep", _i32), ("m", _i32), ("tokens", _p), ("counts", _p), ("tail", _p),
+    ]
+
+
 class WhError(RuntimeError):
     pass
 
@@ -110,6 +117,8 @@ def lib() -> ctypes.CDLL:
         L.wh_top_logprobs.restype = ctypes.c_int
         L.wh_top_logprobs_workspace_bytes.argtypes = [_i32, _i32, _i32]
         L.wh_top_logprobs_workspace_bytes.restype = ctypes.c_size_t
+        L.wh_history_append.argtypes = [ctypes.POINTER(HistoryArgs), _p]
+        L.wh_history_append.restype = ctypes.c_int
         L.wh_verify_force_exact.argtypes = [ctypes.c_int]
         L.wh_verify_force_exact.restype = ctypes.c_int
         L.wh_exp_fix44.argtypes = [_p, _p, _i64, _p]
