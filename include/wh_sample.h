@@ -42,6 +42,13 @@
  *                           `tokens = concat([tokens, y])` and the MTP loop's
  *                           sampling_tokens.append (qwen4_exp.py:1143-1149),
  *                           on a device buffer.
+ *   wh_lmhead_logits        the LM head that produces the logits:
+ *                           model.lm_head(hidden) (model.py:716,
+ *                           dspark.py:313, qwen4_exp.py:960-961), bf16 MFMA.
+ *   wh_lmhead_greedy        the LM head fused with greedy selection (argmax,
+ *                           lowest index among equal maxima; make_sampler at
+ *                           temp 0, dspark.py:326): the logits never reach
+ *                           memory.
  *
  * Random numbers: the reference draws from MLX's global PRNG
  * (mx.random.categorical / uniform, dspark.py:329, 884, 904).  This library
@@ -79,6 +86,7 @@ extern "C" {
 #define WH_MAX_VOCAB 262144      /* V <= 2^18 keeps fixed-point sums below 2^62 */
 #define WH_MAX_WINDOW 4096       /* penalty window entries per row */
 #define WH_MAX_TOP_LOGPROBS 64   /* n of wh_top_logprobs */
+#define WH_LMHEAD_MAX_ROWS 64    /* M of the LM-head entry points */
 
 typedef struct wh_sample_args {
   const void* logits;        /* device, B rows of V values (dtype), row stride in elements */
@@ -252,6 +260,32 @@ typedef struct wh_history_args {
   const int32_t* tail;       /* device, [B], nullable */
 } wh_history_args;
 int wh_history_append(const wh_history_args* args, void* stream);
+
+/* LM head: logits[m, v] = sum_k x[m, k] * weight[v, k], bf16 inputs,
+ * float32 accumulation (MFMA; the summation order is the kernel's, fixed
+ * for given K).  x [M, K] and weight [V, K] are row-major bf16, 16-byte
+ * aligned; K a multiple of 64; M <= WH_LMHEAD_MAX_ROWS.
+ * wh_lmhead_logits writes logits_out [M, logits_stride] (float32).
+ * wh_lmhead_greedy writes tokens [M]: per row the lowest index among the
+ * largest logits -- the argmax of what wh_lmhead_logits writes -- without
+ * writing the logits; it needs wh_lmhead_greedy_workspace_bytes(M, V) bytes
+ * of workspace (8-byte aligned).  Inputs must hold no NaN. */
+typedef struct wh_lmhead_args {
+  const void* x;             /* device, [M, K] bf16 */
+  const void* weight;        /* device, [V, K] bf16 */
+  int32_t M;
+  int32_t K;
+  int32_t V;
+  int32_t reserved;
+  float* logits_out;         /* device, [M, logits_stride] (wh_lmhead_logits) */
+  int64_t logits_stride;     /* elements, >= V */
+  int32_t* tokens;           /* device, [M] (wh_lmhead_greedy) */
+  void* workspace;           /* device (wh_lmhead_greedy) */
+  size_t workspace_bytes;
+} wh_lmhead_args;
+int wh_lmhead_logits(const wh_lmhead_args* args, void* stream);
+size_t wh_lmhead_greedy_workspace_bytes(int32_t M, int32_t V);
+int wh_lmhead_greedy(const wh_lmhead_args* args, void* stream);
 
 /* Test hook: with on != 0, every entry of wh_verify_fused's sliced form
  * takes the exact per-row algorithm that entries the normaliser bounds leave

@@ -46,7 +46,8 @@ def test_struct_layouts_match_ctypes(L, tmp_path):
     lines = []
     for cname, cls in (("wh_sample_args", L.SampleArgs), ("wh_verify_args", L.VerifyArgs), ("wh_markov_args", L.MarkovArgs),
                       ("wh_top_logprobs_args", L.TopLogprobsArgs),
-                      ("wh_history_args", L.HistoryArgs)):
+                      ("wh_history_args", L.HistoryArgs),
+                      ("wh_lmhead_args", L.LmHeadArgs)):
         lines.append(f'printf("%zu\\n", sizeof({cname}));')
         for f in cls._fields_:
             lines.append(f'printf("%zu\\n", offsetof({cname}, {f[0]}));')
@@ -57,7 +58,7 @@ def test_struct_layouts_match_ctypes(L, tmp_path):
     subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(prog), "-o", str(exe)], check=True)
     got = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True).stdout.split()))
     want = []
-    for cls in (L.SampleArgs, L.VerifyArgs, L.MarkovArgs, L.TopLogprobsArgs, L.HistoryArgs):
+    for cls in (L.SampleArgs, L.VerifyArgs, L.MarkovArgs, L.TopLogprobsArgs, L.HistoryArgs, L.LmHeadArgs):
         want.append(ctypes.sizeof(cls))
         want += [getattr(cls, f[0]).offset for f in cls._fields_]
     assert got == want

@@ -1,0 +1,111 @@
+"""The MFMA LM head and its fused greedy selection on the GPU.
+
+Logits: against a float64 product of the same bf16 inputs, within the
+float32 accumulation bound K * 2^-24 * sum |x w| per entry.  Greedy: the
+fused kernel's tokens must equal the lowest-index argmax of the unfused
+logits and the oracle's temperature-0 selection on them, including exact
+ties (duplicated weight rows).  Sampled rows through lm_head_sample must be
+the oracle's tokens on the GPU's logits."""
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+def announce(msg):
+    sys.stderr.write(f"[gpu-case] {msg}\n")
+    sys.stderr.flush()
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from whallm_amd import _lib
+
+    _lib.lib()
+    return torch.device("cuda:0")
+
+
+def _inputs(dev, M, K, V, seed):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = (torch.randn(M, K, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    w = (torch.randn(V, K, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    return x, w
+
+
+@pytest.mark.parametrize("M,K,V", [(1, 256, 1000), (7, 2560, 151936), (33, 512, 5003), (64, 2560, 151936),
+                                   (16, 4096, 129280), (32, 64, 129)])
+def test_lm_head_logits_and_greedy(dev, oracle, M, K, V):
+    from whallm_amd.lmhead import lm_head, lm_head_greedy
+
+    x, w = _inputs(dev, M, K, V, M * 7 + K)
+    if V > 200:
+        w[V - 100] = w[17]  # exact tie with a lower index
+        w[V // 2] = w[V - 3]
+    announce(f"wh_lmhead_logits M={M} K={K} V={V}")
+    got = lm_head(x, w)
+    xd, wd = x.double(), w.double()
+    ref = xd @ wd.T
+    bound = K * 2.0 ** -24 * (xd.abs() @ wd.abs().T) + 1e-30
+    err = (got.double() - ref).abs()
+    assert bool((err <= bound).all()), float((err / bound).max())
+    announce(f"wh_lmhead_greedy M={M} K={K} V={V}")
+    tok = lm_head_greedy(x, w).cpu().numpy()
+    lg = got.cpu().numpy()
+    assert np.array_equal(tok, np.argmax(lg, axis=1).astype(np.int32))  # numpy: first maximum
+    ot, _ = oracle.sample(lg, oracle.make_params(M, temperature=0.0), np.zeros(M, np.float32))
+    assert np.array_equal(tok, ot)
+
+
+def test_lm_head_greedy_exact_ties(dev):
+    """Rows of x that make two vocabulary entries tie exactly: the lower
+    index wins, also when it lies in a later workgroup's columns' reach."""
+    from whallm_amd.lmhead import lm_head, lm_head_greedy
+
+    M, K, V = 5, 512, 40000
+    x, w = _inputs(dev, M, K, V, 99)
+    hot = torch.ones(K, device=dev, dtype=torch.bfloat16)
+    for v in (31000, 129, 39999, 7):
+        w[v] = hot  # identical rows: identical logits
+    x[:] = 0.25
+    announce("wh_lmhead_greedy ties")
+    tok = lm_head_greedy(x, w).cpu().numpy()
+    lg = lm_head(x, w).cpu().numpy()
+    assert np.all(lg[:, 7] == lg[:, 31000])
+    assert np.all(tok == 7)
+
+
+def test_lm_head_sample_paths(dev, oracle):
+    from whallm_amd.lmhead import lm_head, lm_head_sample
+
+    M, K, V = 24, 1024, 151936
+    x, w = _inputs(dev, M, K, V, 5)
+    rng = np.random.default_rng(3)
+    u = rng.random(M, dtype=np.float32)
+    lg = lm_head(x, w).cpu().numpy()
+    kw = dict(temperature=0.9, top_p=0.9, top_k=40, min_p=0.05)
+    announce("lm_head_sample sampled")
+    t = lm_head_sample(x, w, uniforms=torch.from_numpy(u).to(dev), **kw).cpu().numpy()
+    ot, _ = oracle.sample(lg, oracle.make_params(M, chain=0, **kw), u)
+    assert np.array_equal(t, ot)
+    announce("lm_head_sample greedy (fused)")
+    t0 = lm_head_sample(x, w, temperature=0.0).cpu().numpy()
+    assert np.array_equal(t0, np.argmax(lg, axis=1))
+
+
+def test_lm_head_rejects(dev):
+    from whallm_amd.lmhead import lm_head
+
+    x = torch.zeros(2, 100, device=dev, dtype=torch.bfloat16)
+    w = torch.zeros(10, 100, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        lm_head(x, w)  # K not a multiple of 64
+    with pytest.raises(ValueError):
+        lm_head(torch.zeros(65, 128, device=dev, dtype=torch.bfloat16),
+                torch.zeros(10, 128, device=dev, dtype=torch.bfloat16))

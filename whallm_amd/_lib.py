@@ -27,6 +27,7 @@ OUT_LOGPROBS = 0
 OUT_MASKED = 1
 MAX_VOCAB = 262144
 MAX_TOP_LOGPROBS = 64
+LMHEAD_MAX_ROWS = 64
 MAX_WINDOW = 4096
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -81,6 +82,14 @@ class HistoryArgs(ctypes.Structure):
     ]
 
 
+class LmHeadArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", _p), ("weight", _p), ("M", _i32), ("K", _i32), ("V", _i32), ("reserved", _i32),
+        ("logits_out", _p), ("logits_stride", _i64), ("tokens", _p), ("workspace", _p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class WhError(RuntimeError):
     pass
 
@@ -119,6 +128,12 @@ def lib() -> ctypes.CDLL:
         L.wh_top_logprobs_workspace_bytes.restype = ctypes.c_size_t
         L.wh_history_append.argtypes = [ctypes.POINTER(HistoryArgs), _p]
         L.wh_history_append.restype = ctypes.c_int
+        L.wh_lmhead_logits.argtypes = [ctypes.POINTER(LmHeadArgs), _p]
+        L.wh_lmhead_logits.restype = ctypes.c_int
+        L.wh_lmhead_greedy.argtypes = [ctypes.POINTER(LmHeadArgs), _p]
+        L.wh_lmhead_greedy.restype = ctypes.c_int
+        L.wh_lmhead_greedy_workspace_bytes.argtypes = [_i32, _i32]
+        L.wh_lmhead_greedy_workspace_bytes.restype = ctypes.c_size_t
         L.wh_verify_force_exact.argtypes = [ctypes.c_int]
         L.wh_verify_force_exact.restype = ctypes.c_int
         L.wh_exp_fix44.argtypes = [_p, _p, _i64, _p]
