@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--summarize-profile", metavar="OUT", default=None,
+                    help="write profiles/ summaries from a profiling folder (see summarize_profile)")
     return ap.parse_args()
 
 
@@ -153,6 +155,7 @@ def bench_verify(args):
     parity["timed_set0_bit_exact"] = bool(np.array_equal(a1.cpu().numpy(), want_a) and np.array_equal(t1.cpu().numpy(), want_t))
     nbytes = w.bytes_per_call()
     achieved = nbytes / avg_s / 1e9
+    must = w.must_read_bytes(want_a)
     traffic, traffic_src = measured_traffic(3, w.name)
     res = {
         "metric": "verified rows/sec + % of HBM peak, speculative verify at B=16, n=8, V=129,280",
@@ -172,6 +175,7 @@ def bench_verify(args):
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "kernel": "wh_verify_fused", "kernel_avg_us": avg_s * 1e6, "algorithmic_bytes": nbytes,
+                     "must_read_bytes": must, "achieved_must_read": must / avg_s / 1e9,
                      "traffic_source": traffic_src},
         "parity": parity,
     }
@@ -195,18 +199,128 @@ def bench_verify(args):
     print(json.dumps(res))
 
 
+PROFILE_NAMES = {
+    1: "wh_sample_workload1_b1_v129280_f32",
+    2: "wh_sample_workload2_b64_v151936_bf16",
+    3: "wh_verify_fused_workload3_b16_n8_v129280_f32",
+    4: "wh_sample_workload4_b256_v129280_f32_topk",
+    5: "wh_sample_workload5_b128_v151936_bf16_mtp",
+}
+
+
+def traffic_path(workload: int) -> str:
+    return os.path.join(ROOT, "profiles", PROFILE_NAMES[workload] + ".traffic.json")
+
+
 def measured_traffic(workload: int, name: str):
     """HBM bytes per call from the committed rocprofv3 --pmc summary of this
     workload (FETCH_SIZE and WRITE_SIZE runs, each scaled by what the counter
-    reads for a 256 MiB copy), or None when there is none for this workload."""
-    path = os.path.join(ROOT, "profiles", f"wh_sample_workload{workload}_traffic.json")
+    reads for a 256 MiB copy).  None when there is none, when it is for
+    another workload, or when it was measured on other library sources (its
+    recorded source digest differs from this tree's)."""
+    from whallm_amd.build import source_digest
+
+    path = traffic_path(workload)
     if not os.path.exists(path):
         return None, None
     with open(path) as f:
         t = json.load(f)
     if t.get("workload") != name:
         return None, None
+    if t.get("library_digest") != source_digest():
+        return None, f"stale: {os.path.relpath(path, ROOT)} was measured on other library sources"
     return int(t["traffic_bytes_per_call"]), t.get("source")
+
+
+def summarize_profile(workload: int, out: str):
+    """Write profiles/<name>.md and the traffic record bench.py reads from one
+    profiling folder `out`, holding (each from the command listed in the
+    summary): trace/ (--kernel-trace --stats), fetch/ and write/ (--pmc
+    FETCH_SIZE / WRITE_SIZE), copy_fetch/ and copy_write/ (the 256 MiB copy
+    calibration), bench.json (this bench without a profiler) and trace.json
+    (its line under the kernel trace)."""
+    import collections
+    import csv
+    import glob
+
+    from whallm_amd.build import source_digest
+
+    def pmc(d):
+        f = glob.glob(os.path.join(out, d, "**", "*counter_collection.csv"), recursive=True)[0]
+        agg = collections.defaultdict(list)
+        for r in csv.DictReader(open(f)):
+            agg[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+        return agg
+
+    def last_json(fn):
+        return json.loads(open(os.path.join(out, fn)).read().strip().splitlines()[-1])
+
+    cf, cw, bf, bw = pmc("copy_fetch"), pmc("copy_write"), pmc("fetch"), pmc("write")
+    copy = [k for k in cf if "copyBuffer" in k][0]
+    copy_kib = 256 * 1024
+    fscale = copy_kib / (sum(cf[copy]) / len(cf[copy]))
+    wscale = copy_kib / (sum(cw[copy]) / len(cw[copy]))
+    rows, tot = [], 0.0
+    for k in sorted(k for k in bf if "wh::" in k):
+        f = sum(bf[k]) / len(bf[k])
+        w = sum(bw[k]) / len(bw[k])
+        b = (f * fscale + w * wscale) * 1024
+        tot += b
+        rows.append((k.split("(")[0].replace("void ", ""), len(bf[k]), f, w, f * fscale * 1024, w * wscale * 1024))
+    stats = list(csv.DictReader(open(glob.glob(os.path.join(out, "trace", "**", "*kernel_stats.csv"), recursive=True)[0])))
+    bench, tr = last_json("bench.json"), last_json("trace.json")
+    alg = bench["roofline"]["algorithmic_bytes"]
+    name = PROFILE_NAMES[workload]
+    W = workload
+    md = [f"# {bench['roofline']['kernel']}, {bench['config']['workload']}\n",
+          "Commands (one MI355X, repository root; `cd /tmp && export TMPDIR=/tmp` first for rocprofv3; "
+          "OUT is any folder):\n", "```",
+          f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o t -- python3 bench.py --workload {W} "
+          f"--steps 200 --warmup 20 --no-cpu-baseline > OUT/trace.json",
+          f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o b -- python3 bench.py --workload {W} "
+          f"--steps 32 --warmup 4 --no-cpu-baseline",
+          f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o b -- python3 bench.py --workload {W} "
+          f"--steps 32 --warmup 4 --no-cpu-baseline",
+          "rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/copy_fetch -o c -- python3 bench.py --copy-calibration --steps 3",
+          "rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/copy_write -o c -- python3 bench.py --copy-calibration --steps 3",
+          f"python3 bench.py --workload {W} > OUT/bench.json",
+          f"python3 bench.py --summarize-profile OUT --workload {W}", "```\n",
+          f"Library source digest: `{source_digest()}`\n",
+          "## Kernel trace (--kernel-trace --stats)\n", "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    ksum = 0.0
+    for r in stats:
+        if "wh::" not in r["Name"]:
+            continue
+        ksum += float(r["AverageNs"]) / 1000
+        md.append(f"| {r['Name'].split('(')[0].replace('void ', '')} | {r['Calls']} | {float(r['AverageNs']) / 1000:.2f} "
+                  f"| {float(r['MinNs']) / 1000:.2f} | {float(r['MaxNs']) / 1000:.2f} |")
+    md.append(f"\nSum of the kernels' averages: {ksum:.2f} us per call.  The bench without the profiler measured "
+              f"{bench['roofline']['kernel_avg_us']:.2f} us per call with HIP events on the launch stream (every kernel "
+              f"of the call and the gaps between them); under the kernel trace it measured "
+              f"{tr['roofline']['kernel_avg_us']:.2f} us.\n")
+    md += ["## HBM traffic (--pmc, one counter per run)\n",
+           f"Calibration: a 256 MiB device copy (`__amd_rocclr_copyBuffer`) reads FETCH_SIZE "
+           f"{sum(cf[copy]) / len(cf[copy]):.1f} KiB and WRITE_SIZE {sum(cw[copy]) / len(cw[copy]):.1f} KiB per dispatch: "
+           f"scale factors {fscale:.4f} (FETCH_SIZE) and {wscale:.4f} (WRITE_SIZE).\n",
+           "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | read bytes (scaled) | written bytes (scaled) |",
+           "|---|---|---|---|---|---|"]
+    for n, c, f, w, fb, wb in rows:
+        md.append(f"| {n} | {c} | {f:.1f} | {w:.1f} | {fb:,.0f} | {wb:,.0f} |")
+    md.append(f"\nTraffic per call (all kernels): {tot:,.0f} bytes; algorithmic bytes per call {alg:,} "
+              f"(ratio {tot / alg:.3f}).")
+    if "must_read_bytes" in bench["roofline"]:
+        mr = bench["roofline"]["must_read_bytes"]
+        md.append(f"Bytes the call must read (early exit at the first rejection, set 0): {mr:,} (traffic ratio "
+                  f"{tot / mr:.3f}).")
+    md += ["\n## Bench line (no profiler)\n", "```", json.dumps(bench), "```"]
+    with open(os.path.join(ROOT, "profiles", name + ".md"), "w") as f:
+        f.write("\n".join(md) + "\n")
+    with open(traffic_path(workload), "w") as f:
+        json.dump({"workload": bench["config"]["workload"], "traffic_bytes_per_call": round(tot),
+                   "fetch_scale": fscale, "write_scale": wscale, "library_digest": source_digest(),
+                   "kernels": {n: {"fetch_kib": f, "write_kib": w} for n, c, f, w, fb, wb in rows},
+                   "source": f"profiles/{name}.md"}, f, indent=1)
+    print("\n".join(md))
 
 
 def cpu_baseline(w, seconds: float):
@@ -243,6 +357,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.steps)
+        return
+    if args.summarize_profile:
+        summarize_profile(args.workload, args.summarize_profile)
         return
     if args.workload == 3:
         bench_verify(args)

@@ -43,8 +43,29 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP toolchain is required to build libwh_sample.so")
 
 
+def source_digest() -> str:
+    """sha256 over the library's sources (every file under csrc, the public
+    header) and its compiler flags: what a profile was measured on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted(os.listdir(CSRC))
+    for name in files:
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(CSRC, name), "rb") as f:
+                h.update(f.read())
+    with open(os.path.join(ROOT, "include", "wh_sample.h"), "rb") as f:
+        h.update(f.read())
+    h.update(" ".join(SOURCES + HIPCC_FLAGS).encode())
+    return h.hexdigest()
+
+
 def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    missing = [s for s in SOURCES if not os.path.exists(os.path.join(CSRC, s))]
+    if missing:
+        raise RuntimeError(f"library sources missing: {missing}")
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
     tmp = LIB + ".tmp"
     cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, *srcs, "-o", tmp]
     if verbose:

@@ -101,6 +101,16 @@ class VerifyWorkload:
         B, n, V = self.B, self.n, self.V
         return B * (n + 1) * V * 4 + B * n * V * 4 + B * n * 4 + B * (n + 1) * 4 + B * 8
 
+    def must_read_bytes(self, accepted) -> int:
+        """Bytes a verifier that stops at each entry's first rejection must
+        move: every target row (each position's normaliser), the draft
+        probability q(t_j) of every tested draft, the whole q row at a
+        rejection (the residual), ids, uniforms and outputs."""
+        B, n, V = self.B, self.n, self.V
+        rejected = int(sum(1 for a in accepted if a < n))
+        tested = int(sum(min(int(a) + 1, n) for a in accepted))
+        return B * (n + 1) * V * 4 + tested * 4 + rejected * V * 4 + B * n * 4 + B * (n + 1) * 4 + B * 8
+
 
 def _rngs(idx: int):
     return np.random.Generator(np.random.PCG64(SEED0 + idx)), np.random.Generator(np.random.PCG64(SEED0 + idx + 1000))
