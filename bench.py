@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--lmhead", metavar="M,K,V", default=None,
+                    help="time the LM head (wh_lmhead_logits and wh_lmhead_greedy) at this shape instead")
     ap.add_argument("--summarize-profile", metavar="OUT", default=None,
                     help="write profiles/ summaries from a profiling folder (see summarize_profile)")
     return ap.parse_args()
@@ -212,6 +214,62 @@ def traffic_path(workload: int) -> str:
     return os.path.join(ROOT, "profiles", PROFILE_NAMES[workload] + ".traffic.json")
 
 
+def bench_lmhead(args):
+    """The LM head x [M, K] @ W[V, K]^T (bf16, float32 accumulation), alone
+    and fused with greedy selection.  A step is one call; 4 weight copies
+    rotate (beyond the 256 MB Infinity Cache at these shapes).  Roofline:
+    W + x read once and the logits written once, over the HIP-event time per
+    call; the fused form's bytes omit the logits.  Checks the fused tokens
+    against the argmax of the unfused logits first."""
+    import torch
+
+    from whallm_amd import lmhead
+
+    M, K, V = (int(v) for v in args.lmhead.split(","))
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    x = (torch.randn(M, K, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    ws = [(torch.randn(V, K, device=dev, generator=g) * 0.05).to(torch.bfloat16) for _ in range(4)]
+    out = torch.empty(M, V, device=dev)
+    lg = lmhead.lm_head(x, ws[0], out).clone()
+    tok = lmhead.lm_head_greedy(x, ws[0])
+    parity = {"greedy_equals_argmax_of_logits": bool(torch.equal(tok.long(), torch.argmax(lg, dim=1)))}
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        for i in range(args.warmup):
+            fn(ws[i % 4])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(args.steps):
+            fn(ws[i % 4])
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / args.steps, time.perf_counter() - t0
+
+    t_log, wall = timed(lambda w: lmhead.lm_head(x, w, out))
+    t_gr, _ = timed(lambda w: lmhead.lm_head_greedy(x, w))
+    wbytes, xbytes, obytes = V * K * 2, M * K * 2, M * V * 4
+    achieved = (wbytes + xbytes + obytes) / t_log / 1e9
+    res = {
+        "metric": "LM head rows/sec + % of HBM peak", "value": M * args.steps / wall, "unit": "rows/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall / args.steps * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16 (fp32 accumulate)",
+        "data": "synthetic", "config": {"workload": f"lm_head M={M} K={K} V={V}", "M": M, "K": K, "V": V,
+                                         "weight_copies": 4, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None, "kernel": "lmhead_logits_kernel",
+                     "kernel_avg_us": t_log * 1e6, "algorithmic_bytes": wbytes + xbytes + obytes},
+        "fused_greedy": {"kernel_avg_us": t_gr * 1e6, "algorithmic_bytes": wbytes + xbytes + M * 4,
+                         "achieved": (wbytes + xbytes + M * 4) / t_gr / 1e9},
+        "parity": parity,
+    }
+    print(json.dumps(res))
+
+
 def measured_traffic(workload: int, name: str):
     """HBM bytes per call from the committed rocprofv3 --pmc summary of this
     workload (FETCH_SIZE and WRITE_SIZE runs, each scaled by what the counter
@@ -232,7 +290,7 @@ def measured_traffic(workload: int, name: str):
     return int(t["traffic_bytes_per_call"]), t.get("source")
 
 
-def summarize_profile(workload: int, out: str):
+def summarize_profile(workload: int, out: str, lmhead: str | None = None):
     """Write profiles/<name>.md and the traffic record bench.py reads from one
     profiling folder `out`, holding (each from the command listed in the
     summary): trace/ (--kernel-trace --stats), fetch/ and write/ (--pmc
@@ -261,7 +319,7 @@ def summarize_profile(workload: int, out: str):
     fscale = copy_kib / (sum(cf[copy]) / len(cf[copy]))
     wscale = copy_kib / (sum(cw[copy]) / len(cw[copy]))
     rows, tot = [], 0.0
-    for k in sorted(k for k in bf if "wh::" in k):
+    for k in sorted(k for k in bf if "wh::" in k and "greedy" not in k):
         f = sum(bf[k]) / len(bf[k])
         w = sum(bw[k]) / len(bw[k])
         b = (f * fscale + w * wscale) * 1024
@@ -270,21 +328,26 @@ def summarize_profile(workload: int, out: str):
     stats = list(csv.DictReader(open(glob.glob(os.path.join(out, "trace", "**", "*kernel_stats.csv"), recursive=True)[0])))
     bench, tr = last_json("bench.json"), last_json("trace.json")
     alg = bench["roofline"]["algorithmic_bytes"]
-    name = PROFILE_NAMES[workload]
-    W = workload
+    if lmhead:
+        M, K, V = lmhead.split(",")
+        name = f"wh_lmhead_m{M}_k{K}_v{V}"
+        run = f"--lmhead {lmhead}"
+        steps, psteps = "--steps 20 --warmup 5", "--steps 4 --warmup 1"
+    else:
+        name = PROFILE_NAMES[workload]
+        run = f"--workload {workload}"
+        steps, psteps = "--steps 200 --warmup 20 --no-cpu-baseline", "--steps 32 --warmup 4 --no-cpu-baseline"
     md = [f"# {bench['roofline']['kernel']}, {bench['config']['workload']}\n",
           "Commands (one MI355X, repository root; `cd /tmp && export TMPDIR=/tmp` first for rocprofv3; "
           "OUT is any folder):\n", "```",
-          f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o t -- python3 bench.py --workload {W} "
-          f"--steps 200 --warmup 20 --no-cpu-baseline > OUT/trace.json",
-          f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o b -- python3 bench.py --workload {W} "
-          f"--steps 32 --warmup 4 --no-cpu-baseline",
-          f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o b -- python3 bench.py --workload {W} "
-          f"--steps 32 --warmup 4 --no-cpu-baseline",
+          f"rocprofv3 --kernel-trace --stats --output-format csv -d OUT/trace -o t -- python3 bench.py {run} "
+          f"{steps} > OUT/trace.json",
+          f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -o b -- python3 bench.py {run} {psteps}",
+          f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -o b -- python3 bench.py {run} {psteps}",
           "rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/copy_fetch -o c -- python3 bench.py --copy-calibration --steps 3",
           "rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/copy_write -o c -- python3 bench.py --copy-calibration --steps 3",
-          f"python3 bench.py --workload {W} > OUT/bench.json",
-          f"python3 bench.py --summarize-profile OUT --workload {W}", "```\n",
+          f"python3 bench.py {run}{' ' + steps if lmhead else ''} > OUT/bench.json",
+          f"python3 bench.py --summarize-profile OUT {run}", "```\n",
           f"Library source digest: `{source_digest()}`\n",
           "## Kernel trace (--kernel-trace --stats)\n", "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
     ksum = 0.0
@@ -294,7 +357,11 @@ def summarize_profile(workload: int, out: str):
         ksum += float(r["AverageNs"]) / 1000
         md.append(f"| {r['Name'].split('(')[0].replace('void ', '')} | {r['Calls']} | {float(r['AverageNs']) / 1000:.2f} "
                   f"| {float(r['MinNs']) / 1000:.2f} | {float(r['MaxNs']) / 1000:.2f} |")
-    md.append(f"\nSum of the kernels' averages: {ksum:.2f} us per call.  The bench without the profiler measured "
+    if lmhead:
+        md.append("\nThe bench calls each entry point in turn (the logits kernel; the greedy kernel and its "
+                  "per-row reduction).")
+    md.append(f"\nSum of the kernels' averages: {ksum:.2f} us{' (both entry points)' if lmhead else ' per call'}.  "
+              f"The bench without the profiler measured "
               f"{bench['roofline']['kernel_avg_us']:.2f} us per call with HIP events on the launch stream (every kernel "
               f"of the call and the gaps between them); under the kernel trace it measured "
               f"{tr['roofline']['kernel_avg_us']:.2f} us.\n")
@@ -306,8 +373,8 @@ def summarize_profile(workload: int, out: str):
            "|---|---|---|---|---|---|"]
     for n, c, f, w, fb, wb in rows:
         md.append(f"| {n} | {c} | {f:.1f} | {w:.1f} | {fb:,.0f} | {wb:,.0f} |")
-    md.append(f"\nTraffic per call (all kernels): {tot:,.0f} bytes; algorithmic bytes per call {alg:,} "
-              f"(ratio {tot / alg:.3f}).")
+    md.append(f"\nTraffic per call ({'the logits kernel' if lmhead else 'all kernels'}): {tot:,.0f} bytes; "
+              f"algorithmic bytes per call {alg:,} (ratio {tot / alg:.3f}).")
     if "must_read_bytes" in bench["roofline"]:
         mr = bench["roofline"]["must_read_bytes"]
         md.append(f"Bytes the call must read (early exit at the first rejection, set 0): {mr:,} (traffic ratio "
@@ -315,6 +382,9 @@ def summarize_profile(workload: int, out: str):
     md += ["\n## Bench line (no profiler)\n", "```", json.dumps(bench), "```"]
     with open(os.path.join(ROOT, "profiles", name + ".md"), "w") as f:
         f.write("\n".join(md) + "\n")
+    if lmhead:
+        print("\n".join(md))
+        return
     with open(traffic_path(workload), "w") as f:
         json.dump({"workload": bench["config"]["workload"], "traffic_bytes_per_call": round(tot),
                    "fetch_scale": fscale, "write_scale": wscale, "library_digest": source_digest(),
@@ -359,7 +429,10 @@ def main():
         copy_calibration(args.steps)
         return
     if args.summarize_profile:
-        summarize_profile(args.workload, args.summarize_profile)
+        summarize_profile(args.workload, args.summarize_profile, args.lmhead)
+        return
+    if args.lmhead:
+        bench_lmhead(args)
         return
     if args.workload == 3:
         bench_verify(args)

@@ -12,15 +12,18 @@
 // weight, row v is vocabulary entry v), K a multiple of 64.  At decode sizes
 // the product is bound by the one pass over W (V*K*2 bytes: 778 MB for
 // V = 151,936, K = 2560), so the kernel is built to stream W:
-//   * a workgroup owns 128 vocabulary rows; per step it reads a 64- or
-//     128-k slab of them with coalesced 16-byte loads (consecutive lanes on
-//     consecutive bytes of a row) and stages it, with the same k of x,
-//     through LDS; the next slab is in registers while this one computes;
+//   * a workgroup of NWV waves owns 32 * NWV vocabulary rows; per step it
+//     reads a 64-k slab of them with coalesced 16-byte loads (consecutive
+//     lanes on consecutive bytes of a row) and stages it, with the same k of
+//     x, through LDS; the next slab is in registers while this one computes;
 //   * each wave multiplies its 32 rows by every x row (one or two 32-row
 //     blocks) with v_mfma_f32_32x32x16_bf16, float32 accumulation; the
-//     fragments come from LDS, so every W byte crosses HBM once.
+//     fragments come from LDS, so every W byte crosses HBM once;
+//   * x is re-read from L2 by every workgroup, so with two x row blocks the
+//     workgroup is 8 waves (256 rows: half the x traffic of 4 waves); with
+//     one block, 4 waves (more workgroups, better balance).
 // (Loading MFMA fragments straight from memory -- 32 rows per load
-// instruction -- ran at 1.1-2.1 TB/s; the staged form at 3.4-6.4 TB/s.)
+// instruction -- ran at 1.1-2.1 TB/s; the staged form at 3.4-6.5 TB/s.)
 // Epilogues: (a) the float32 logits, (b) greedy: per row the largest
 // (value, lowest index) key of the workgroup's 128 columns, written to a
 // partials buffer; wh_lmhead_greedy's second kernel reduces them per row.
@@ -35,8 +38,8 @@ namespace wh {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int LM_T = 256;          // threads per workgroup (four waves)
-constexpr int LM_COLS = 128;       // vocabulary rows per workgroup (32 per wave)
+constexpr int LM_KS = 64;          // k per pipeline step
+constexpr int LM_MIN_COLS = 128;   // vocabulary rows per workgroup, at least (4 waves)
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& q) {
   bf16x8 r;
@@ -44,31 +47,31 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& q) {
   return r;
 }
 
-// LDS tiles of one pipeline step: KS k of the workgroup's 128 W rows and of
-// the 32 * MB x rows, rows padded by 16 bytes (fragment reads of 32 rows at
-// one k then fall on distinct bank groups).
-template <int MB, int KS>
+// LDS tiles of one pipeline step: KS k of the workgroup's 32 * NWV W rows
+// and of the 32 * MB x rows, rows padded by 16 bytes (fragment reads of 32
+// rows at one k then fall on distinct bank groups).
+template <int MB, int KS, int NWV>
 struct LmSmem {
   static constexpr int RS = KS * 2 + 16;
-  char w[LM_COLS * RS];
+  char w[32 * NWV * RS];
   char x[32 * MB * RS];
 };
 
 // Accumulate x[rows] . W[cols] over K for the wave's 32 columns
 // (row0 + 32 * wave ..) and all 32 * MB x rows.  Per step the workgroup
-// loads KS k of its 128 W rows with coalesced 16-byte loads (KS * 2 / 16
+// loads KS k of its 32 * NWV W rows with coalesced 16-byte loads (KS * 2 / 16
 // lanes per row, consecutive lanes on consecutive bytes) and the same k of
 // x, stores both to LDS, and each wave reads its MFMA fragments from there.
 // The next step's loads are in registers while the current step computes.
 // Two accumulators per row block (the two 16-k halves of every 32 k) keep
 // consecutive MFMAs independent; the result is their sum.
-template <int MB, int KS>
+template <int MB, int KS, int NWV>
 __device__ __forceinline__ void lm_tile(const char* __restrict__ x, const char* __restrict__ w, int M, int K, int V,
-                                        int row0, LmSmem<MB, KS>& sm, f32x16 (&res)[MB]) {
-  constexpr int RS = LmSmem<MB, KS>::RS;
+                                        int row0, LmSmem<MB, KS, NWV>& sm, f32x16 (&res)[MB]) {
+  constexpr int RS = LmSmem<MB, KS, NWV>::RS;
   constexpr int LPR = KS * 2 / 16;          // lanes per row
-  constexpr int WR = LM_T / LPR;            // rows per load round
-  constexpr int NW = LM_COLS / WR;          // W load rounds
+  constexpr int WR = 64 * NWV / LPR;        // rows per load round
+  constexpr int NW = 32 * NWV / WR;         // W load rounds
   constexpr int XR = 32 * MB;
   constexpr int NX = (XR + WR - 1) / WR;    // x load rounds
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6, h = lane >> 5, r = lane & 31;
@@ -133,15 +136,15 @@ __device__ __forceinline__ void lm_tile(const char* __restrict__ x, const char* 
 // the 32-row block, column l % 32.
 __device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
-template <int MB, int KS>
-__global__ void __launch_bounds__(LM_T) lmhead_logits_kernel(const char* __restrict__ x, const char* __restrict__ w,
-                                                             float* __restrict__ out, long long ldo, int M, int K,
-                                                             int V) {
-  __shared__ __align__(16) LmSmem<MB, KS> sm;
+template <int MB, int KS, int NWV>
+__global__ void __launch_bounds__(64 * NWV) lmhead_logits_kernel(const char* __restrict__ x, const char* __restrict__ w,
+                                                                 float* __restrict__ out, long long ldo, int M, int K,
+                                                                 int V) {
+  __shared__ __align__(16) LmSmem<MB, KS, NWV> sm;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int col0 = blockIdx.x * LM_COLS + wv * 32;
+  const int col0 = blockIdx.x * 32 * NWV + wv * 32;
   f32x16 acc[MB];
-  lm_tile<MB, KS>(x, w, M, K, V, blockIdx.x * LM_COLS, sm, acc);
+  lm_tile<MB, KS, NWV>(x, w, M, K, V, blockIdx.x * 32 * NWV, sm, acc);
   const int col = col0 + (lane & 31);
   if (col >= V) return;
 #pragma unroll
@@ -158,35 +161,43 @@ __device__ __forceinline__ uint64_t greedy_key(float v, int col) {
   return ((uint64_t)fkey(v + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)col);
 }
 
-template <int MB, int KS>
-__global__ void __launch_bounds__(LM_T) lmhead_greedy_kernel(const char* __restrict__ x, const char* __restrict__ w,
-                                                             uint64_t* __restrict__ part, int M, int K, int V) {
-  __shared__ __align__(16) LmSmem<MB, KS> sm;
-  __shared__ uint64_t red[LM_T / 64][64];
+template <int MB, int KS, int NWV>
+__global__ void __launch_bounds__(64 * NWV) lmhead_greedy_kernel(const char* __restrict__ x, const char* __restrict__ w,
+                                                                 uint64_t* __restrict__ part, int M, int K, int V) {
+  __shared__ __align__(16) LmSmem<MB, KS, NWV> sm;
+  __shared__ uint64_t red[NWV][64];
+  static_assert(sizeof(sm.w) >= NWV * 32 * 33 * sizeof(float), "greedy transpose region");
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int col0 = blockIdx.x * LM_COLS + wv * 32;
+  const int col0 = blockIdx.x * 32 * NWV + wv * 32;
   f32x16 acc[MB];
-  lm_tile<MB, KS>(x, w, M, K, V, blockIdx.x * LM_COLS, sm, acc);
-  const int col = col0 + (lane & 31);
+  lm_tile<MB, KS, NWV>(x, w, M, K, V, blockIdx.x * 32 * NWV, sm, acc);
+  // Per row, the largest key of the wave's 32 columns: the wave writes its
+  // 32 x 32 block of each row block to its own LDS region (the tile loop's
+  // buffers, free after its final barrier; rows 33 floats apart), then lane
+  // r < 32 scans row r.  (Reducing 64-bit keys across lanes with shuffles
+  // cost more than the logits' store.)
+  float* reg = (float*)sm.w + wv * (32 * 33);
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      uint64_t k = col < V ? greedy_key(acc[mb][i], col) : 0;
-      // max over the 32 lanes of this half (same row, the wave's 32 columns)
-#pragma unroll
-      for (int o = 16; o >= 1; o >>= 1) {
-        const uint64_t y = __shfl_xor(k, o, 64);
+    for (int i = 0; i < 16; ++i) reg[acc_row(i, lane) * 33 + (lane & 31)] = acc[mb][i];
+    __syncthreads();
+    if (lane < 32) {
+      uint64_t k = 0;
+#pragma unroll 8
+      for (int c = 0; c < 32; ++c) {
+        const uint64_t y = col0 + c < V ? greedy_key(reg[lane * 33 + c], col0 + c) : 0;
         k = y > k ? y : k;
       }
-      if ((lane & 31) == 0) red[wv][32 * mb + acc_row(i, lane)] = k;
+      red[wv][32 * mb + lane] = k;
     }
-  __syncthreads();
+    __syncthreads();
+  }
   if (threadIdx.x < 32 * MB) {
     const int row = threadIdx.x;
     uint64_t k = red[0][row];
 #pragma unroll
-    for (int q = 1; q < LM_T / 64; ++q) k = red[q][row] > k ? red[q][row] : k;
+    for (int q = 1; q < NWV; ++q) k = red[q][row] > k ? red[q][row] : k;
     if (row < M) part[(size_t)row * gridDim.x + blockIdx.x] = k;
   }
 }
@@ -225,7 +236,9 @@ static int lm_check(const wh_lmhead_args* a) {
   return WH_OK;
 }
 
-static int lm_blocks(int V) { return (V + LM_COLS - 1) / LM_COLS; }
+// Workgroups of a launch (vocabulary rows per workgroup: 32 * NWV); the
+// greedy partials are sized for the narrowest workgroup.
+static int lm_blocks(int V, int cols) { return (V + cols - 1) / cols; }
 
 }  // namespace wh
 
@@ -239,16 +252,15 @@ extern "C" int wh_lmhead_logits(const wh_lmhead_args* a, void* stream) {
   if (!a->logits_out) return fail(WH_EINVAL, "logits_out is required");
   if (a->logits_stride < a->V) return fail(WH_EINVAL, "logits_stride (%lld) must be >= V (%d)", (long long)a->logits_stride, a->V);
   hipStream_t st = (hipStream_t)stream;
-  const dim3 g(lm_blocks(a->V));
   const char *x = (const char*)a->x, *w = (const char*)a->weight;
   const long long ldo = a->logits_stride;
-  // one x row block: 64-k steps; two: 128-k steps where K allows
+  // one x row block: 4 waves (128 rows); two: 8 waves (256 rows)
   if (a->M <= 32)
-    hipLaunchKernelGGL((lmhead_logits_kernel<1, 64>), g, dim3(LM_T), 0, st, x, w, a->logits_out, ldo, a->M, a->K, a->V);
-  else if (a->K % 128 == 0)
-    hipLaunchKernelGGL((lmhead_logits_kernel<2, 128>), g, dim3(LM_T), 0, st, x, w, a->logits_out, ldo, a->M, a->K, a->V);
+    hipLaunchKernelGGL((lmhead_logits_kernel<1, LM_KS, 4>), dim3(lm_blocks(a->V, 128)), dim3(256), 0, st, x, w,
+                       a->logits_out, ldo, a->M, a->K, a->V);
   else
-    hipLaunchKernelGGL((lmhead_logits_kernel<2, 64>), g, dim3(LM_T), 0, st, x, w, a->logits_out, ldo, a->M, a->K, a->V);
+    hipLaunchKernelGGL((lmhead_logits_kernel<2, LM_KS, 8>), dim3(lm_blocks(a->V, 256)), dim3(512), 0, st, x, w,
+                       a->logits_out, ldo, a->M, a->K, a->V);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "lmhead_logits_kernel launch failed: %s", hipGetErrorString(e));
   return WH_OK;
@@ -256,7 +268,7 @@ extern "C" int wh_lmhead_logits(const wh_lmhead_args* a, void* stream) {
 
 extern "C" size_t wh_lmhead_greedy_workspace_bytes(int32_t M, int32_t V) {
   if (M <= 0 || V <= 0) return 0;
-  return (size_t)M * lm_blocks(V) * sizeof(uint64_t);
+  return (size_t)M * lm_blocks(V, LM_MIN_COLS) * sizeof(uint64_t);
 }
 
 extern "C" int wh_lmhead_greedy(const wh_lmhead_args* a, void* stream) {
@@ -265,20 +277,21 @@ extern "C" int wh_lmhead_greedy(const wh_lmhead_args* a, void* stream) {
   if (rc) return rc;
   if (a->M == 0) return WH_OK;
   if (!a->tokens) return fail(WH_EINVAL, "tokens is required");
-  const size_t need = (size_t)a->M * lm_blocks(a->V) * sizeof(uint64_t);
+  const size_t need = (size_t)a->M * lm_blocks(a->V, LM_MIN_COLS) * sizeof(uint64_t);
   if (!a->workspace || a->workspace_bytes < need)
     return fail(WH_EINVAL, "workspace must hold wh_lmhead_greedy_workspace_bytes(M, V) = %zu bytes", need);
   if ((uintptr_t)a->workspace % 8) return fail(WH_EINVAL, "workspace must be 8-byte aligned");
   hipStream_t st = (hipStream_t)stream;
-  const int nwg = lm_blocks(a->V);
   uint64_t* part = (uint64_t*)a->workspace;
   const char *x = (const char*)a->x, *w = (const char*)a->weight;
-  if (a->M <= 32)
-    hipLaunchKernelGGL((lmhead_greedy_kernel<1, 64>), dim3(nwg), dim3(LM_T), 0, st, x, w, part, a->M, a->K, a->V);
-  else if (a->K % 128 == 0)
-    hipLaunchKernelGGL((lmhead_greedy_kernel<2, 128>), dim3(nwg), dim3(LM_T), 0, st, x, w, part, a->M, a->K, a->V);
-  else
-    hipLaunchKernelGGL((lmhead_greedy_kernel<2, 64>), dim3(nwg), dim3(LM_T), 0, st, x, w, part, a->M, a->K, a->V);
+  int nwg;
+  if (a->M <= 32) {
+    nwg = lm_blocks(a->V, 128);
+    hipLaunchKernelGGL((lmhead_greedy_kernel<1, LM_KS, 4>), dim3(nwg), dim3(256), 0, st, x, w, part, a->M, a->K, a->V);
+  } else {
+    nwg = lm_blocks(a->V, 256);
+    hipLaunchKernelGGL((lmhead_greedy_kernel<2, LM_KS, 8>), dim3(nwg), dim3(512), 0, st, x, w, part, a->M, a->K, a->V);
+  }
   hipLaunchKernelGGL(lmhead_greedy_final, dim3(a->M), dim3(256), 0, st, (const uint64_t*)part, nwg, a->tokens);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "lmhead greedy launch failed: %s", hipGetErrorString(e));
