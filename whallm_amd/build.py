@@ -19,7 +19,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libwh_sample.so")
-SOURCES = ["wh_sample.hip", "wh_verify.hip", "wh_fast.hip", "wh_draft.hip", "wh_logprobs.hip", "wh_history.hip", "wh_lmhead.hip"]
+SOURCES = ["wh_sample.hip", "wh_verify.hip", "wh_fast.hip", "wh_draft.hip", "wh_logprobs.hip", "wh_history.hip", "wh_lmhead.hip", "wh_wide.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

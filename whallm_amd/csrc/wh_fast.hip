@@ -1708,7 +1708,7 @@ static WsLayout ws_layout(int B, const HostPlan& p) {
 // (penalties can take more slices for the codes to fit in LDS).
 size_t sample_workspace_bytes(int B, int V) {
   if (B <= 0 || V <= 0) return 256;
-  size_t t = 0;
+  size_t t = wide_workspace_bytes(B, V);
   for (int dt : {WH_DTYPE_F32, WH_DTYPE_BF16})
     for (int hc : {0, 2 * WH_MAX_WINDOW}) t = std::max(t, ws_layout(B, make_plan(B, V, dt, hc)).total);
   return t;
@@ -1777,6 +1777,10 @@ static int launch_merge(const SampleKArgs& k, const FastPlan& fp, size_t lds, hi
 }
 
 int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st) {
+  // top-p alone, or no filter: candidates cannot bound the kept set, so the
+  // wide exact engine (many workgroups per row) takes the rows
+  if (wide_applicable(k0) && p->workspace && p->workspace_bytes >= wide_workspace_bytes(k0.B, k0.V))
+    return launch_sample_wide(k0, p, st);
   const int esz = k0.dtype == WH_DTYPE_BF16 ? 2 : 4;
   HostPlan hp = make_plan(k0.B, k0.V, k0.dtype, k0.hcap);
   WsLayout wl = ws_layout(k0.B, hp);

@@ -48,5 +48,8 @@ size_t penalty_lds_bytes(const SampleKArgs& k);
 size_t sample_workspace_bytes(int B, int V);
 int launch_sample(const SampleKArgs& k, const wh_sample_args* p, hipStream_t st);
 int launch_sample_exact(const SampleKArgs& k, hipStream_t st);
+bool wide_applicable(const SampleKArgs& k);
+size_t wide_workspace_bytes(int B, int V);
+int launch_sample_wide(const SampleKArgs& k, const wh_sample_args* p, hipStream_t st);
 
 }  // namespace wh

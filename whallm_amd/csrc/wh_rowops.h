@@ -36,6 +36,11 @@ struct RowCtx {
     if (hmask >= 0 && ((bitmap[i >> 5] >> (i & 31)) & 1u)) return lookup(i);
     return raw(i) + 0.0f;
   }
+  // The same from an already loaded raw(i).
+  __device__ __forceinline__ float val_from(int i, float r) const {
+    if (hmask >= 0 && ((bitmap[i >> 5] >> (i & 31)) & 1u)) return lookup(i);
+    return r + 0.0f;
+  }
 };
 
 // Filter state: an element is kept iff every active predicate holds.
