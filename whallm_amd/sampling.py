@@ -247,10 +247,11 @@ class SampleCall:
 
 
 def last_paths(device, B: int) -> torch.Tensor:
-    """Per-row engine path of the last sliced-engine call on the current
-    stream's workspace: 0 merged from candidates, 1 exact engine (candidate
-    overflow or no filter), 2 greedy, 3 exact engine (top-p cut not settled
-    by the normaliser bounds).  Diagnostics only: results are identical."""
+    """Per-row engine path of the last workspace call on the current
+    stream: 0 merged from candidates, 1 exact engine (candidate or list
+    overflow), 2 greedy, 3 exact engine (top-p cut not settled by the
+    normaliser bounds), 6 wide exact engine (top-p alone or no filter).
+    Diagnostics only: results are identical."""
     ws = L.workspace(torch.device(device), 0)
     return ws[:4 * B].view(torch.int32).clone()
 
