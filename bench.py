@@ -252,6 +252,17 @@ def bench_lmhead(args):
 
     t_log, wall = timed(lambda w: lmhead.lm_head(x, w, out))
     t_gr, _ = timed(lambda w: lmhead.lm_head_greedy(x, w))
+    # sampled rows at the reference's defaults (T 0.2, top-p 0.98): the fused
+    # call against the product, then the sampler
+    from whallm_amd import sampling
+
+    u = torch.rand(M, device=dev, generator=g)
+    dflt = dict(temperature=0.2, top_p=0.98)
+    t_sf, _ = timed(lambda w: lmhead.lm_head_sample(x, w, uniforms=u, **dflt))
+    t_su, _ = timed(lambda w: sampling.sample(lmhead.lm_head(x, w, out), uniforms=u, **dflt))
+    ft = lmhead.lm_head_sample(x, ws[0], uniforms=u, **dflt)
+    parity["sampled_fused_equals_unfused"] = bool(torch.equal(ft, sampling.sample(lmhead.lm_head(x, ws[0], out),
+                                                                                  uniforms=u, **dflt)))
     wbytes, xbytes, obytes = V * K * 2, M * K * 2, M * V * 4
     achieved = (wbytes + xbytes + obytes) / t_log / 1e9
     res = {
@@ -265,6 +276,7 @@ def bench_lmhead(args):
                      "kernel_avg_us": t_log * 1e6, "algorithmic_bytes": wbytes + xbytes + obytes},
         "fused_greedy": {"kernel_avg_us": t_gr * 1e6, "algorithmic_bytes": wbytes + xbytes + M * 4,
                          "achieved": (wbytes + xbytes + M * 4) / t_gr / 1e9},
+        "sampled_T0.2_p0.98": {"fused_us": t_sf * 1e6, "lm_head_then_sample_us": t_su * 1e6},
         "parity": parity,
     }
     print(json.dumps(res))

@@ -49,6 +49,11 @@
  *                           lowest index among equal maxima; make_sampler at
  *                           temp 0, dspark.py:326): the logits never reach
  *                           memory.
+ *   wh_lmhead_sample        the LM head, then wh_sample on its logits; for
+ *                           rows filtered by top-p alone or not at all (the
+ *                           reference's defaults, generation.py:109-118),
+ *                           the product's epilogue also emits the per-slice
+ *                           maxima the sampler's first step would compute.
  *
  * Random numbers: the reference draws from MLX's global PRNG
  * (mx.random.categorical / uniform, dspark.py:329, 884, 904).  This library
@@ -286,6 +291,15 @@ typedef struct wh_lmhead_args {
 int wh_lmhead_logits(const wh_lmhead_args* args, void* stream);
 size_t wh_lmhead_greedy_workspace_bytes(int32_t M, int32_t V);
 int wh_lmhead_greedy(const wh_lmhead_args* args, void* stream);
+/* wh_lmhead_logits into args->logits_out, then wh_sample on those logits:
+ * `sample` carries the sampling parameters and outputs (its logits, dtype,
+ * B, V and row_stride are ignored: the logits are args'); results equal the
+ * two calls made in turn.  Rows with a temperature above 0 whose only filter
+ * is top-p (or none), without penalties or per-row temperatures, and a
+ * workspace of wh_sample_workspace_bytes(M, V), take the fused form: the
+ * product also merges each row's (value, index) maxima per sampler slice,
+ * and the sampler starts after its max step. */
+int wh_lmhead_sample(const wh_lmhead_args* args, const wh_sample_args* sample, void* stream);
 
 /* Test hook: with on != 0, every entry of wh_verify_fused's sliced form
  * takes the exact per-row algorithm that entries the normaliser bounds leave

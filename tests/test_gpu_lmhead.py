@@ -109,3 +109,47 @@ def test_lm_head_rejects(dev):
     with pytest.raises(ValueError):
         lm_head(torch.zeros(65, 128, device=dev, dtype=torch.bfloat16),
                 torch.zeros(10, 128, device=dev, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("M,K,V", [(1, 2560, 151936), (16, 1024, 129280), (64, 2560, 151936), (33, 512, 5003)])
+def test_lm_head_sample_fused_wide(dev, oracle, M, K, V):
+    """Rows filtered by top-p alone (or not at all): the product emits the
+    sampler's slice maxima.  Tokens equal lm_head() then sample(), and the
+    oracle on the same logits; the logits themselves are the product's."""
+    from whallm_amd import sampling
+    from whallm_amd.lmhead import lm_head, lm_head_sample
+
+    x, w = _inputs(dev, M, K, V, 300 + M)
+    ref = lm_head(x, w)
+    lg = ref.cpu().numpy()
+    rng = np.random.default_rng(M + V)
+    for chain, T, top_p in ((0, 0.2, 0.98), (1, 1.0, 0.9), (0, 0.7, 1.0)):
+        u = rng.random(M, dtype=np.float32)
+        ut = torch.from_numpy(u).to(dev)
+        kw = dict(temperature=T, top_p=top_p, chain="mlx" if chain == 0 else "whallm")
+        announce(f"wh_lmhead_sample fused M={M} K={K} V={V} {kw}")
+        tok, logits = lm_head_sample(x, w, uniforms=ut, return_logits=True, **kw)
+        assert torch.equal(logits, ref)
+        assert set(sampling.last_paths(dev, M).cpu().numpy().tolist()) <= {6, 1}
+        unf = sampling.sample(ref, uniforms=ut, **kw)
+        ot, _ = oracle.sample(lg, oracle.make_params(M, temperature=T, top_p=top_p, chain=chain), u)
+        assert np.array_equal(tok.cpu().numpy(), unf.cpu().numpy())
+        assert np.array_equal(tok.cpu().numpy(), ot)
+
+
+def test_lm_head_sample_unfused_routes(dev, oracle):
+    """Penalties (the epilogue sees raw logits) take the product, then the
+    sampler; the tokens still match the oracle."""
+    from whallm_amd.lmhead import lm_head, lm_head_sample
+
+    M, K, V = 8, 512, 30000
+    x, w = _inputs(dev, M, K, V, 41)
+    lg = lm_head(x, w).cpu().numpy()
+    rng = np.random.default_rng(2)
+    hist = rng.integers(0, V, (M, 64)).astype(np.int32)
+    u = rng.random(M, dtype=np.float32)
+    kw = dict(temperature=0.8, top_p=0.95, presence_penalty=0.5, presence_context=32)
+    announce("wh_lmhead_sample with penalties")
+    tok = lm_head_sample(x, w, uniforms=torch.from_numpy(u).to(dev), history=torch.from_numpy(hist).to(dev), **kw)
+    ot, _ = oracle.sample(lg, oracle.make_params(M, chain=0, **kw), u, hist)
+    assert np.array_equal(tok.cpu().numpy(), ot)

@@ -132,6 +132,8 @@ def lib() -> ctypes.CDLL:
         L.wh_lmhead_logits.restype = ctypes.c_int
         L.wh_lmhead_greedy.argtypes = [ctypes.POINTER(LmHeadArgs), _p]
         L.wh_lmhead_greedy.restype = ctypes.c_int
+        L.wh_lmhead_sample.argtypes = [ctypes.POINTER(LmHeadArgs), ctypes.POINTER(SampleArgs), _p]
+        L.wh_lmhead_sample.restype = ctypes.c_int
         L.wh_lmhead_greedy_workspace_bytes.argtypes = [_i32, _i32]
         L.wh_lmhead_greedy_workspace_bytes.restype = ctypes.c_size_t
         L.wh_verify_force_exact.argtypes = [ctypes.c_int]

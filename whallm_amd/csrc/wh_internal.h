@@ -51,5 +51,7 @@ int launch_sample_exact(const SampleKArgs& k, hipStream_t st);
 bool wide_applicable(const SampleKArgs& k);
 size_t wide_workspace_bytes(int B, int V);
 int launch_sample_wide(const SampleKArgs& k, const wh_sample_args* p, hipStream_t st);
+int wide_keys_prepare(const SampleKArgs& k, void* workspace, hipStream_t st, uint64_t** keys, int* G, int* SL);
+int launch_sample_wide_from_keys(const SampleKArgs& k, const wh_sample_args* p, hipStream_t st);
 
 }  // namespace wh

@@ -161,21 +161,16 @@ __device__ __forceinline__ uint64_t greedy_key(float v, int col) {
   return ((uint64_t)fkey(v + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)col);
 }
 
+// Per row, the largest key of the workgroup's columns into red[wave][row]:
+// each wave writes its 32 x 32 block of each row block to its own LDS region
+// (the tile loop's buffers, free after its final barrier; rows 33 floats
+// apart), then lane r < 32 scans row r.  (Reducing 64-bit keys across lanes
+// with shuffles cost more than the logits' store.)
 template <int MB, int KS, int NWV>
-__global__ void __launch_bounds__(64 * NWV) lmhead_greedy_kernel(const char* __restrict__ x, const char* __restrict__ w,
-                                                                 uint64_t* __restrict__ part, int M, int K, int V) {
-  __shared__ __align__(16) LmSmem<MB, KS, NWV> sm;
-  __shared__ uint64_t red[NWV][64];
-  static_assert(sizeof(sm.w) >= NWV * 32 * 33 * sizeof(float), "greedy transpose region");
+__device__ __forceinline__ void lm_row_keys(const f32x16 (&acc)[MB], LmSmem<MB, KS, NWV>& sm, uint64_t (*red)[64],
+                                            int col0, int V) {
+  static_assert(sizeof(sm.w) >= NWV * 32 * 33 * sizeof(float), "key transpose region");
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int col0 = blockIdx.x * 32 * NWV + wv * 32;
-  f32x16 acc[MB];
-  lm_tile<MB, KS, NWV>(x, w, M, K, V, blockIdx.x * 32 * NWV, sm, acc);
-  // Per row, the largest key of the wave's 32 columns: the wave writes its
-  // 32 x 32 block of each row block to its own LDS region (the tile loop's
-  // buffers, free after its final barrier; rows 33 floats apart), then lane
-  // r < 32 scans row r.  (Reducing 64-bit keys across lanes with shuffles
-  // cost more than the logits' store.)
   float* reg = (float*)sm.w + wv * (32 * 33);
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -193,12 +188,59 @@ __global__ void __launch_bounds__(64 * NWV) lmhead_greedy_kernel(const char* __r
     }
     __syncthreads();
   }
+}
+
+template <int MB, int KS, int NWV>
+__global__ void __launch_bounds__(64 * NWV) lmhead_greedy_kernel(const char* __restrict__ x, const char* __restrict__ w,
+                                                                 uint64_t* __restrict__ part, int M, int K, int V) {
+  __shared__ __align__(16) LmSmem<MB, KS, NWV> sm;
+  __shared__ uint64_t red[NWV][64];
+  const int wv = threadIdx.x >> 6;
+  f32x16 acc[MB];
+  lm_tile<MB, KS, NWV>(x, w, M, K, V, blockIdx.x * 32 * NWV, sm, acc);
+  lm_row_keys<MB, KS, NWV>(acc, sm, red, blockIdx.x * 32 * NWV + wv * 32, V);
   if (threadIdx.x < 32 * MB) {
     const int row = threadIdx.x;
     uint64_t k = red[0][row];
 #pragma unroll
     for (int q = 1; q < NWV; ++q) k = red[q][row] > k ? red[q][row] : k;
     if (row < M) part[(size_t)row * gridDim.x + blockIdx.x] = k;
+  }
+}
+
+// The logits, plus each row's largest key over the workgroup's columns
+// merged (atomic max) into keys[row * G + slice] of the wide sampler, whose
+// slices (SL entries, a multiple of 32 * NWV) each hold whole workgroups.
+template <int MB, int KS, int NWV>
+__global__ void __launch_bounds__(64 * NWV) lmhead_slicemax_kernel(const char* __restrict__ x,
+                                                                   const char* __restrict__ w,
+                                                                   float* __restrict__ out, long long ldo, int M,
+                                                                   int K, int V, uint64_t* __restrict__ keys, int G,
+                                                                   int SL) {
+  __shared__ __align__(16) LmSmem<MB, KS, NWV> sm;
+  __shared__ uint64_t red[NWV][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int col0 = blockIdx.x * 32 * NWV + wv * 32;
+  f32x16 acc[MB];
+  lm_tile<MB, KS, NWV>(x, w, M, K, V, blockIdx.x * 32 * NWV, sm, acc);
+  const int col = col0 + (lane & 31);
+  if (col < V) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int row = 32 * mb + acc_row(i, lane);
+        if (row < M) out[(size_t)row * ldo + col] = acc[mb][i];
+      }
+  }
+  lm_row_keys<MB, KS, NWV>(acc, sm, red, col0, V);
+  if (threadIdx.x < 32 * MB) {
+    const int row = threadIdx.x;
+    uint64_t k = red[0][row];
+#pragma unroll
+    for (int q = 1; q < NWV; ++q) k = red[q][row] > k ? red[q][row] : k;
+    if (row < M && k) atomicMax((unsigned long long*)&keys[(size_t)row * G + blockIdx.x * 32 * NWV / SL],
+                                (unsigned long long)k);
   }
 }
 
@@ -296,4 +338,51 @@ extern "C" int wh_lmhead_greedy(const wh_lmhead_args* a, void* stream) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "lmhead greedy launch failed: %s", hipGetErrorString(e));
   return WH_OK;
+}
+
+extern "C" int wh_lmhead_sample(const wh_lmhead_args* lm, const wh_sample_args* sp, void* stream) {
+  clear_error();
+  int rc = lm_check(lm);
+  if (rc) return rc;
+  if (!sp) return fail(WH_EINVAL, "sample args is NULL");
+  if (lm->M == 0) return WH_OK;
+  if (!lm->logits_out) return fail(WH_EINVAL, "logits_out is required (the sampler reads the logits)");
+  if (lm->logits_stride < lm->V)
+    return fail(WH_EINVAL, "logits_stride (%lld) must be >= V (%d)", (long long)lm->logits_stride, lm->V);
+  wh_sample_args s = *sp;
+  s.logits = lm->logits_out;
+  s.dtype = WH_DTYPE_F32;
+  s.B = lm->M;
+  s.V = lm->V;
+  s.row_stride = lm->logits_stride;
+  SampleKArgs k;
+  rc = prepare_sample(&s, &k, true);
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  // rows the wide sampler takes, without penalties (the epilogue sees the
+  // raw logits) and with one temperature: the product writes their slice
+  // maxima, and the sampler starts from its histogram step
+  const bool fuse = wide_applicable(k) && k.hcap == 0 && !k.T_rows && s.workspace &&
+                    s.workspace_bytes >= wide_workspace_bytes(k.B, k.V);
+  if (!fuse) {
+    rc = wh_lmhead_logits(lm, stream);
+    if (rc) return rc;
+    if (!s.tokens && !s.logprobs_out && !s.kept_count) return WH_OK;
+    return launch_sample(k, &s, st);
+  }
+  uint64_t* keys = nullptr;
+  int G = 0, SL = 0;
+  rc = wide_keys_prepare(k, s.workspace, st, &keys, &G, &SL);
+  if (rc) return rc;
+  const char *x = (const char*)lm->x, *w = (const char*)lm->weight;
+  const long long ldo = lm->logits_stride;
+  if (lm->M <= 32)
+    hipLaunchKernelGGL((lmhead_slicemax_kernel<1, LM_KS, 4>), dim3(lm_blocks(lm->V, 128)), dim3(256), 0, st, x, w,
+                       lm->logits_out, ldo, lm->M, lm->K, lm->V, keys, G, SL);
+  else
+    hipLaunchKernelGGL((lmhead_slicemax_kernel<2, LM_KS, 8>), dim3(lm_blocks(lm->V, 256)), dim3(512), 0, st, x, w,
+                       lm->logits_out, ldo, lm->M, lm->K, lm->V, keys, G, SL);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(WH_EHIP, "lmhead_slicemax_kernel launch failed: %s", hipGetErrorString(e));
+  return launch_sample_wide_from_keys(k, &s, st);
 }

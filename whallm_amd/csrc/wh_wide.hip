@@ -70,6 +70,9 @@ struct WxPtrs {
   int* list_i;        // [B * WX_CAP]
   int* lcnt;          // [B]
   WxRec* rec;         // [B]
+  // [B * G] (value key << 32 | ~index) maxima per slice, written by the LM
+  // head's epilogue in place of the max step (nullptr otherwise)
+  uint64_t* part_key;
   int G;              // slices per row
   int SL;             // entries per slice (256 * E)
 };
@@ -146,8 +149,24 @@ __device__ __forceinline__ void wx_slice(const SampleKArgs& a, int b, int lo, in
 // Row max from the slice maxima (every thread returns it).
 __device__ __forceinline__ float wx_row_max(const WxPtrs& P, int b, float* scratch) {
   float m = -INFINITY;
-  for (int g = threadIdx.x; g < P.G; g += blockDim.x) m = fmaxf(m, P.part_m[(size_t)b * P.G + g]);
+  for (int g = threadIdx.x; g < P.G; g += blockDim.x) {
+    if (P.part_key) {
+      const uint64_t k = P.part_key[(size_t)b * P.G + g];
+      m = fmaxf(m, k ? key_to_float((uint32_t)(k >> 32)) : -INFINITY);
+    } else {
+      m = fmaxf(m, P.part_m[(size_t)b * P.G + g]);
+    }
+  }
   return block_reduce(m, scratch, OpMaxF(), -INFINITY);
+}
+
+// Before an LM head that writes the slice maxima itself: clear them, the
+// histograms and the list counters (the max step's other duties).
+__global__ void __launch_bounds__(WX_T) wx_init_kernel(WxPtrs P, int B) {
+  const size_t i = (size_t)blockIdx.x * WX_T + threadIdx.x;
+  if (i < (size_t)B * P.G) P.part_key[i] = 0;
+  if (i < (size_t)B * WX_BINS) P.hist_w[i] = 0;
+  if (i < (size_t)B) P.lcnt[i] = 0;
 }
 
 __device__ __forceinline__ int wx_bin(float m, float l) {
@@ -556,7 +575,7 @@ static int wx_entries(int B) { return B <= 8 ? 4 : 16; }
 static int wx_slices(int V, int E) { return (V + WX_T * E - 1) / (WX_T * E); }
 
 struct WxLayout {
-  size_t path, part_m, part_i, part_vw, part_n, hist_w, list_v, list_i, lcnt, rec, total;
+  size_t path, part_m, part_i, part_vw, part_n, hist_w, list_v, list_i, lcnt, rec, part_key, total;
 };
 
 // Sized for the most slices any batch size uses (1024-entry slices).
@@ -575,6 +594,7 @@ static WxLayout wx_layout(int B, int V) {
   l.list_i = o;  o = al(o + Bz * WX_CAP * 4);
   l.lcnt = o;    o = al(o + Bz * 4);
   l.rec = o;     o = al(o + Bz * sizeof(WxRec));
+  l.part_key = o; o = al(o + Bz * G * 8);
   l.total = o;
   return l;
 }
@@ -599,7 +619,7 @@ static int wx_lds(const void* fn, size_t lds) {
 }
 
 template <int E>
-static int wx_launch(const SampleKArgs& k, WxPtrs P, hipStream_t st) {
+static int wx_launch(const SampleKArgs& k, WxPtrs P, hipStream_t st, bool from_keys) {
   const bool any_p = k.top_p_rows || (k.top_p > 0.0 && k.top_p < 1.0);
   // slice workgroups: the penalty table of one slice's id range
   const size_t lds_s = k.hcap > 0 ? (size_t)k.hcap * 12 + (size_t)(WX_T * E / 32) * 4 : 0;
@@ -611,7 +631,7 @@ static int wx_launch(const SampleKArgs& k, WxPtrs P, hipStream_t st) {
       (rc = wx_lds((const void*)wx_rows_kernel<E>, lds_s)))
     return rc;
   const dim3 gs(P.G, k.B);
-  hipLaunchKernelGGL(wx_max_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
+  if (!from_keys) hipLaunchKernelGGL(wx_max_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
   if (any_p) {
     hipLaunchKernelGGL(wx_hist_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
     hipLaunchKernelGGL(wx_collect_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
@@ -627,9 +647,9 @@ static int wx_launch(const SampleKArgs& k, WxPtrs P, hipStream_t st) {
   return WH_OK;
 }
 
-int launch_sample_wide(const SampleKArgs& k, const wh_sample_args* p, hipStream_t st) {
+static WxPtrs wx_ptrs_of(const SampleKArgs& k, void* workspace) {
   const WxLayout L = wx_layout(k.B, k.V);
-  char* ws = (char*)p->workspace;
+  char* ws = (char*)workspace;
   const int E = wx_entries(k.B);
   WxPtrs P;
   P.SL = WX_T * E;
@@ -644,8 +664,36 @@ int launch_sample_wide(const SampleKArgs& k, const wh_sample_args* p, hipStream_
   P.list_i = (int*)(ws + L.list_i);
   P.lcnt = (int*)(ws + L.lcnt);
   P.rec = (WxRec*)(ws + L.rec);
+  P.part_key = nullptr;
+  return P;
+}
+
+int launch_sample_wide(const SampleKArgs& k, const wh_sample_args* p, hipStream_t st) {
+  WxPtrs P = wx_ptrs_of(k, p->workspace);
   if (P.G > WX_MAXG) return fail(WH_ELIMIT, "too many slices for the wide engine");
-  return E == 4 ? wx_launch<4>(k, P, st) : wx_launch<16>(k, P, st);
+  return P.SL == WX_T * 4 ? wx_launch<4>(k, P, st, false) : wx_launch<16>(k, P, st, false);
+}
+
+// The wide engine after an LM head that writes the slice maxima: the keys'
+// array, slice count and length for the head, cleared on the stream first.
+int wide_keys_prepare(const SampleKArgs& k, void* workspace, hipStream_t st, uint64_t** keys, int* G, int* SL) {
+  WxPtrs P = wx_ptrs_of(k, workspace);
+  if (P.G > WX_MAXG) return fail(WH_ELIMIT, "too many slices for the wide engine");
+  P.part_key = (uint64_t*)((char*)workspace + wx_layout(k.B, k.V).part_key);
+  const size_t n = std::max((size_t)k.B * WX_BINS, (size_t)k.B * P.G);
+  hipLaunchKernelGGL(wx_init_kernel, dim3((unsigned)((n + WX_T - 1) / WX_T)), dim3(WX_T), 0, st, P, k.B);
+  *keys = P.part_key;
+  *G = P.G;
+  *SL = P.SL;
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(WH_EHIP, "wide engine launch failed: %s", hipGetErrorString(e));
+  return WH_OK;
+}
+
+int launch_sample_wide_from_keys(const SampleKArgs& k, const wh_sample_args* p, hipStream_t st) {
+  WxPtrs P = wx_ptrs_of(k, p->workspace);
+  P.part_key = (uint64_t*)((char*)p->workspace + wx_layout(k.B, k.V).part_key);
+  return P.SL == WX_T * 4 ? wx_launch<4>(k, P, st, true) : wx_launch<16>(k, P, st, true);
 }
 
 }  // namespace wh

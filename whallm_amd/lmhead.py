@@ -6,8 +6,9 @@ qwen4_exp.py:960-961).  lm_head() computes them (wh_lmhead_logits, bf16
 inputs, float32 accumulation); lm_head_greedy() fuses the product with
 temperature-0 selection (wh_lmhead_greedy: argmax, lowest index among equal
 maxima) so the logits never reach memory; lm_head_sample() takes sample()'s
-arguments and uses the fused path where it applies (temperature 0, no
-penalties), otherwise lm_head() then sample().
+arguments: temperature 0 without penalties takes the fused greedy kernel,
+rows filtered by top-p alone (or not at all) take the product with the
+sampler's first step in its epilogue, the rest the product then the sampler.
 """
 from __future__ import annotations
 
@@ -66,13 +67,49 @@ def lm_head_greedy(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 _PENALTIES = ("repetition_penalty", "presence_penalty", "frequency_penalty")
 
 
-def lm_head_sample(x: torch.Tensor, weight: torch.Tensor, **sample_kwargs) -> torch.Tensor:
-    """sample(lm_head(x, weight), **sample_kwargs); temperature 0 without
-    penalties (and no row-wise parameters) takes the fused greedy kernel."""
-    greedy = not (sample_kwargs.get("temperature", 0.0) > 0.0)
-    plain = not any(sample_kwargs.get(k) for k in _PENALTIES) and not any(
-        sample_kwargs.get(k) is not None for k in ("temperature_rows", "top_p_rows", "min_p_rows", "top_k_rows"))
-    extra = sample_kwargs.get("return_logprobs") or sample_kwargs.get("return_kept")
-    if greedy and plain and not extra:
+def lm_head_sample(x: torch.Tensor, weight: torch.Tensor, *, temperature: float = 0.0, top_p: float = 1.0,
+                   top_k: int = 0, min_p: float = 0.0, chain="mlx", uniforms: torch.Tensor | None = None,
+                   generator: torch.Generator | None = None, return_logits: bool = False, **kw):
+    """sample(lm_head(x, weight), ...) in one call (wh_lmhead_sample).
+
+    Temperature 0 without penalties or row-wise parameters takes the fused
+    greedy kernel (no logits written).  Rows filtered by top-p alone or not
+    at all, without penalties, take the fused sampled form: the product also
+    emits the sampler's per-slice maxima.  Otherwise the product, then the
+    sampler.  Returns int32 tokens [M] (and the float32 logits with
+    return_logits)."""
+    plain = not any(kw.get(k) for k in _PENALTIES) and not any(
+        kw.get(k) is not None for k in ("temperature_rows", "top_p_rows", "min_p_rows", "top_k_rows"))
+    if not (temperature > 0.0) and plain and not return_logits and not any(kw.values()):
         return lm_head_greedy(x, weight)
-    return S.sample(lm_head(x, weight), **sample_kwargs)
+    a = _args(x, weight)
+    M, V = a.M, a.V
+    dev = x.device
+    logits = torch.empty(M, V, dtype=torch.float32, device=dev)
+    a.logits_out = logits.data_ptr()
+    a.logits_stride = V
+    if uniforms is None:
+        uniforms = torch.rand(M, device=dev, dtype=torch.float32, generator=generator)
+    uniforms = torch.as_tensor(uniforms, dtype=torch.float32, device=dev).reshape(M).contiguous()
+    tokens = torch.empty(M, dtype=torch.int32, device=dev)
+    sa = L.SampleArgs()
+    rows = (S._rows_param(kw.pop("temperature_rows", None), M, torch.float64, dev),
+            S._rows_param(kw.pop("top_p_rows", None), M, torch.float64, dev),
+            S._rows_param(kw.pop("min_p_rows", None), M, torch.float64, dev),
+            S._rows_param(kw.pop("top_k_rows", None), M, torch.int32, dev))
+    keep = S._fill_args(sa, logits, L.DTYPE_F32, chain, kw.pop("history", None), kw.pop("history_len", None),
+                        temperature, top_p, top_k, min_p, kw.pop("repetition_penalty", 0.0),
+                        kw.pop("presence_penalty", 0.0), kw.pop("frequency_penalty", 0.0),
+                        kw.pop("repetition_context", 20), kw.pop("presence_context", 20),
+                        kw.pop("frequency_context", 20), rows)
+    if kw:
+        raise TypeError(f"unexpected arguments: {sorted(kw)}")
+    sa.uniforms = uniforms.data_ptr()
+    sa.tokens = tokens.data_ptr()
+    sa.out_mode = L.OUT_LOGPROBS
+    ws = L.workspace(dev, L.lib().wh_sample_workspace_bytes(M, V))
+    sa.workspace = ws.data_ptr()
+    sa.workspace_bytes = ws.numel()
+    L.check(L.lib().wh_lmhead_sample(ctypes.byref(a), ctypes.byref(sa), ctypes.c_void_p(L.stream_of(x))))
+    del keep
+    return (tokens, logits) if return_logits else tokens
