@@ -154,3 +154,36 @@ def test_history_append_mtp_commit(dev):
             new = list(drafts[b, :min(max(acc[b], 0), n)]) + [int(nxt[b])]
             model[b] = model[b] + new if len(model[b]) + len(new) <= cap else model[b][-keep:] + new
     assert st.rows() == [[int(v) for v in row] for row in model]
+
+
+def test_default_options_loop_matches_oracle(dev, oracle):
+    """The reference's default request (T 0.2, top-p 0.98, no top-k / min-p;
+    generation.py:109-118) at V = 151,936, one sequence: the rows take the
+    wide exact engine; tokens identical to the oracle at every step."""
+    from whallm_amd.decode import GenerationOptions, TokenSelector, generate
+
+    Vq = 151936
+    rng = np.random.default_rng(21)
+    table = rng.normal(0, 2.0, (16, Vq)).astype(np.float32)
+    opts = GenerationOptions(presence_penalty=0.3, repetition_penalty=1.1)
+    sel = TokenSelector.from_options(opts)
+    steps = 24
+    U = rng.random((steps, 1), dtype=np.float32)
+    prompt = [[11, 12, 13, 11]]
+    p = oracle.make_params(1, chain=0, temperature=0.2, top_p=0.98, presence_penalty=0.3, repetition_penalty=1.1,
+                           presence_context=20, repetition_context=20)
+    hist = list(prompt[0])
+    want = []
+    last = prompt[0][-1]
+    for s in range(steps):
+        x = table[last % 16][None]
+        tok, _ = oracle.sample(x, p, U[s], np.array([hist], np.int32), np.array([len(hist)], np.int32))
+        want.append([int(tok[0])])
+        hist.append(int(tok[0]))
+        last = int(tok[0])
+    tab = torch.from_numpy(table).to(dev)
+    Ud = torch.from_numpy(U).to(dev)
+    announce("decode loop, default options, V=151936")
+    got = list(generate(lambda l: tab[l.long() % 16], prompt, max_tokens=steps, selector=sel,
+                        uniforms=lambda s: Ud[s]))
+    assert got == want

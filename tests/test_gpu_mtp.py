@@ -84,3 +84,32 @@ def test_mtp_target_rows_and_verify(dev, oracle, seed):
     oa, ot = oracle.verify_logprobs(dl, r.reshape(B, n + 1, V), drafts, u, T)
     assert np.array_equal(acc.cpu().numpy(), oa)
     assert np.array_equal(tok.cpu().numpy(), ot)
+
+
+def test_mtp_rows_qwen_vocabulary(dev, oracle):
+    """The MTP target rows at Qwen's production vocabulary (V = 248,320,
+    qwen4_exp.py:44): penalties over history + drafts[:i], chain B."""
+    from whallm_amd import mtp
+
+    rng = np.random.default_rng(248)
+    B, n, V, H = 2, 3, 248320, 40
+    logits = rng.normal(0, 2.0, (B, n + 1, V)).astype(np.float32)
+    hist = rng.integers(0, V, (B, H + n)).astype(np.int32)  # room for the drafts after the committed ids
+    hlen = np.array([H, 17], np.int32)
+    drafts = rng.integers(0, V, (B, n)).astype(np.int32)
+    kw = dict(temperature=0.6, top_p=0.8, top_k=20, min_p=0.02, repetition_penalty=1.05, presence_penalty=0.4)
+    sys.stderr.write("[gpu-case] mtp rows V=248320\n")
+    rows = mtp.adjusted_logprobs_rows(torch.from_numpy(logits).to(dev), torch.from_numpy(hist).to(dev),
+                                      torch.from_numpy(hlen).to(dev), torch.from_numpy(drafts).to(dev), **kw)
+    rows = rows.cpu().numpy().reshape(B, n + 1, V)
+    p = oracle.make_params(1, chain=1, temperature=0.6, top_p=0.8, top_k=20, min_p=0.02, repetition_penalty=1.05,
+                           presence_penalty=0.4, repetition_context=20, presence_context=20)
+    for b in range(B):
+        for i in range(n + 1):
+            h = np.concatenate([hist[b, :hlen[b]], drafts[b, :i]]).astype(np.int32)
+            _, _, orow = oracle.sample(logits[b, i][None], p, np.zeros(1, np.float32), h[None],
+                                       np.array([h.size], np.int32), want_rows=True)
+            fin = np.isfinite(orow[0])
+            assert np.array_equal(np.isfinite(rows[b, i]), fin)
+            assert np.allclose(np.exp(rows[b, i][fin].astype(np.float64)), np.exp(orow[0][fin].astype(np.float64)),
+                               rtol=1e-5, atol=1e-12)

@@ -22,6 +22,7 @@ once per step to yield Python ints, as generate_step's `.item()` does.
 from __future__ import annotations
 
 import ctypes
+from dataclasses import dataclass
 from typing import Callable, Iterator, Optional, Sequence
 
 import torch
@@ -29,6 +30,22 @@ import torch
 from . import _lib as L
 from . import sampling as S
 from .logprobs import top_logprobs as _top_logprobs
+
+
+@dataclass(frozen=True)
+class GenerationOptions:
+    """The sampling fields of the reference's per-request options
+    (runtime/deepseek_v4_ssd/generation.py:109-118), same names and
+    defaults: temperature 0.2, top-p 0.98, no top-k or min-p, presence 0,
+    repetition 1."""
+
+    max_tokens: int = 272_000
+    temperature: float = 0.2
+    top_p: float = 0.98
+    top_k: int = 0
+    min_p: float = 0.0
+    presence_penalty: float = 0.0
+    repetition_penalty: float = 1.0
 
 
 class DecodeState:
@@ -129,6 +146,16 @@ class TokenSelector:
                                (self.pen["frequency_penalty"], frequency_context)) if p]
         # ids the history must keep: None = the whole history (a context of 0)
         self.window = None if any(c <= 0 for c in ctxs) else max(ctxs, default=0)
+
+    @classmethod
+    def from_options(cls, options: GenerationOptions, **kw) -> "TokenSelector":
+        """The sampler and processors generation.py:1279-1293 builds from a
+        request's options: make_sampler(temp, top_p, top_k, min_p), plus
+        presence / repetition processors when they differ from 0 / 1 (the
+        processors' default window of 20 ids)."""
+        return cls(temperature=options.temperature, top_p=options.top_p, top_k=options.top_k,
+                   min_p=options.min_p, presence_penalty=options.presence_penalty,
+                   repetition_penalty=options.repetition_penalty, chain="mlx", **kw)
 
     @property
     def penalised(self) -> bool:
