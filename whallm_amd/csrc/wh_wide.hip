@@ -161,12 +161,17 @@ __device__ __forceinline__ float wx_row_max(const WxPtrs& P, int b, float* scrat
 }
 
 // Before an LM head that writes the slice maxima itself: clear them, the
-// histograms and the list counters (the max step's other duties).
+// histograms and the list counters, and set the records (the max step's
+// other duties).
 __global__ void __launch_bounds__(WX_T) wx_init_kernel(WxPtrs P, int B) {
   const size_t i = (size_t)blockIdx.x * WX_T + threadIdx.x;
   if (i < (size_t)B * P.G) P.part_key[i] = 0;
   if (i < (size_t)B * WX_BINS) P.hist_w[i] = 0;
-  if (i < (size_t)B) P.lcnt[i] = 0;
+  if (i < (size_t)B) {
+    P.lcnt[i] = 0;
+    P.rec[i].flags = 0;
+    P.path[i] = WX_PATH;
+  }
 }
 
 __device__ __forceinline__ int wx_bin(float m, float l) {
@@ -206,7 +211,13 @@ __global__ void __launch_bounds__(WX_T) wx_max_kernel(SampleKArgs a, WxPtrs P) {
     P.part_i[(size_t)b * P.G + g] = is;
   }
   for (int j = g * WX_T + tid; j < WX_BINS; j += P.G * WX_T) P.hist_w[(size_t)b * WX_BINS + j] = 0;
-  if (g == 0 && tid == 0) P.lcnt[b] = 0;
+  if (g == 0 && tid == 0) {
+    P.lcnt[b] = 0;
+    // rows without top-p need no resolve step: their record is ready here
+    // (the collect and resolve steps rewrite it for the others)
+    P.rec[b].flags = 0;
+    P.path[b] = WX_PATH;
+  }
 }
 
 template <int E>
@@ -636,8 +647,10 @@ static int wx_launch(const SampleKArgs& k, WxPtrs P, hipStream_t st, bool from_k
     hipLaunchKernelGGL(wx_hist_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
     hipLaunchKernelGGL(wx_collect_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
   }
-  // the resolve step also sets every row's flags for the steps after it
-  hipLaunchKernelGGL(wx_resolve_kernel, dim3(k.B), dim3(1024), lds_r, st, k, P);
+  // the resolve step settles rows with top-p and greedy rows; without
+  // either (a scalar temperature above 0 and no top-p) the max step's
+  // records stand
+  if (any_p || k.T_rows) hipLaunchKernelGGL(wx_resolve_kernel, dim3(k.B), dim3(1024), lds_r, st, k, P);
   hipLaunchKernelGGL(wx_drawsum_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
   hipLaunchKernelGGL(wx_pick_kernel<E>, dim3(k.B), dim3(WX_T), lds_s, st, k, P);
   if (k.out_rows && k.out_mode == WH_OUT_LOGPROBS)
