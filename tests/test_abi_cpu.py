@@ -181,3 +181,41 @@ def test_decode_state_host_checks():
     assert sel.window == 32 and sel.penalised
     assert TokenSelector(presence_penalty=0.5, presence_context=0).window is None
     assert not TokenSelector(repetition_penalty=1.0).penalised
+
+
+def test_lmhead_validation(L):
+    a = L.LmHeadArgs()
+    a.x, a.weight, a.logits_out, a.tokens = 1 << 20, 1 << 20, 1 << 20, 1 << 20
+    a.M, a.K, a.V, a.logits_stride = 4, 512, 1000, 1000
+    for kw, code, needle in ((dict(M=65), L.WH_ELIMIT, "M must"), (dict(K=100), L.WH_EINVAL, "K must"),
+                             (dict(V=0), L.WH_ELIMIT, "V must"), (dict(x=(1 << 20) + 8), L.WH_EINVAL, "aligned"),
+                             (dict(logits_stride=999), L.WH_EINVAL, "logits_stride")):
+        b = L.LmHeadArgs.from_buffer_copy(a)
+        for k, v in kw.items():
+            setattr(b, k, v)
+        assert L.lib().wh_lmhead_logits(ctypes.byref(b), None) == code, kw
+        assert needle in L.lib().wh_last_error().decode()
+    # the greedy form needs its workspace
+    assert L.lib().wh_lmhead_greedy(ctypes.byref(a), None) == L.WH_EINVAL
+    assert "workspace" in L.lib().wh_last_error().decode()
+    assert L.lib().wh_lmhead_greedy_workspace_bytes(4, 1000) == 4 * 8 * 8
+    # the fused call validates both halves before any launch
+    s = _args(L, B=4, V=1000, row_stride=1000, tokens=1 << 20, uniforms=None)
+    assert L.lib().wh_lmhead_sample(ctypes.byref(a), ctypes.byref(s), None) == L.WH_EINVAL
+    assert "uniforms" in L.lib().wh_last_error().decode()
+    b = L.LmHeadArgs.from_buffer_copy(a)
+    b.logits_out = None
+    assert L.lib().wh_lmhead_sample(ctypes.byref(b), ctypes.byref(s), None) == L.WH_EINVAL
+
+
+def test_markov_validation(L):
+    a = L.MarkovArgs()
+    a.base, a.embed, a.proj, a.prev, a.logits_out = 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20
+    a.dtype, a.V, a.rank = L.DTYPE_BF16, 1000, 256
+    for kw, needle in ((dict(rank=12), "rank"), (dict(rank=264), "rank"), (dict(dtype=5), "dtype"),
+                       (dict(proj=(1 << 20) + 2), "aligned"), (dict(prev=None), "NULL")):
+        b = L.MarkovArgs.from_buffer_copy(a)
+        for k, v in kw.items():
+            setattr(b, k, v)
+        assert L.lib().wh_markov_logits(ctypes.byref(b), None) in (L.WH_EINVAL, L.WH_ELIMIT), kw
+        assert needle in L.lib().wh_last_error().decode()
