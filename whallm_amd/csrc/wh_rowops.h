@@ -397,8 +397,11 @@ __device__ __forceinline__ float chain_scale(int chain, float d, float invT, dou
 }
 
 // The whole exact algorithm for row b by one workgroup (64..1024 threads, a
-// power of two).
-__device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_smem, ExactSmem& sm) {
+// power of two).  Inlined where it is the kernel's main path, so that its LDS
+// pointers stay LDS pointers; exact_row below is the out-of-line copy for
+// the kernels that reach it only as a fallback (there its LDS accesses are
+// flat accesses through generic pointers).
+__device__ __forceinline__ void exact_row_impl(const SampleKArgs& a, int b, char* dyn_smem, ExactSmem& sm) {
   const int tid = threadIdx.x, nt = blockDim.x;
   const int V = a.V;
   RowCtx rc;
@@ -545,6 +548,10 @@ __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_sm
       out[i] = pr.keep(i, l) ? (float)((double)chain_scale(a.chain, l - m, invT, rTc) - lz) : -INFINITY;
     }
   }
+}
+
+__device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_smem, ExactSmem& sm) {
+  exact_row_impl(a, b, dyn_smem, sm);
 }
 
 }  // namespace wh

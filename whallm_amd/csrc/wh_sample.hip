@@ -24,7 +24,7 @@ namespace wh {
 __global__ void __launch_bounds__(1024) sample_exact_kernel(SampleKArgs a) {
   extern __shared__ __align__(16) char dyn_smem[];
   __shared__ ExactSmem sm;
-  exact_row(a, blockIdx.x, dyn_smem, sm);
+  exact_row_impl(a, blockIdx.x, dyn_smem, sm);
 }
 
 // In-place penalty processors (the unfused drop-in for make_logits_processors).
