@@ -335,13 +335,25 @@ __global__ void __launch_bounds__(WX_T) wx_collect_kernel(SampleKArgs a, WxPtrs 
 }
 
 // Rows with nothing kept: token 0, count 0, every row entry -inf.
-__device__ void wx_none(const SampleKArgs& a, int b) {
+__device__ __forceinline__ void wx_none(const SampleKArgs& a, int b) {
   if (threadIdx.x == 0) {
     if (a.tokens) a.tokens[b] = 0;
     if (a.kept) a.kept[b] = 0;
   }
   if (a.out_rows)
     for (int i = threadIdx.x; i < a.V; i += blockDim.x) a.out_rows[(long long)b * a.V + i] = -INFINITY;
+}
+
+// The resolve kernel's arguments in place in the kernel-argument segment:
+// the out-of-line exact_row reads them through this pointer, so the kernel
+// need not copy its by-value arguments into private memory for it.
+struct ResolveKernArgs {
+  SampleKArgs a;
+  WxPtrs P;
+};
+static_assert(offsetof(ResolveKernArgs, a) == 0, "resolve kernel argument layout");
+__device__ __forceinline__ const ResolveKernArgs* resolve_kernargs() {
+  return (const ResolveKernArgs*)__builtin_amdgcn_kernarg_segment_ptr();
 }
 
 __global__ void __launch_bounds__(1024) wx_resolve_kernel(SampleKArgs a, WxPtrs P) {
@@ -386,7 +398,7 @@ __global__ void __launch_bounds__(1024) wx_resolve_kernel(SampleKArgs a, WxPtrs 
   const int n = P.lcnt[b];
   if (n > WX_CAP) {
     // the boundary bin overflowed the list: the whole exact algorithm
-    exact_row(a, b, dyn, esm);
+    exact_row(resolve_kernargs()->a, b, dyn, esm);
     if (tid == 0) {
       rec->flags = WX_DONE;
       P.path[b] = 1;
