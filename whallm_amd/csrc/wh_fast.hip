@@ -59,7 +59,8 @@ constexpr int GPREF = 4;          // slices per row preferred for small batches
 constexpr int GMAX = 6;           // slices per row the merge is compiled for
 constexpr int FAST_CAP = 2048;    // candidate capacity per slice
 constexpr int RUNGS = 8;          // thresholds per ladder round
-constexpr int LADDER_ROUNDS = 5;  // ladder rounds at most (the first, a far one, refinements)
+constexpr int LADDER_ROUNDS = 2;  // ladder rounds at most (the first, then a far one or the top-p refinement)
+constexpr int HB_BINS = 1024;     // top-k refinement: histogram bins over the ladder's bracket
 constexpr int QM = 16;            // merge: candidate slots per lane, at most
 constexpr int MW = 8;             // merge: waves per workgroup
 constexpr int QW = 2;             // merge: candidate chunks each wave loads with the summaries
@@ -247,6 +248,9 @@ struct SliceSmem {
   float redm[FNW];
   int redg[FNW];
   int lad[LADDER_ROUNDS][RUNGS];  // ladder totals per round (zeroed at kernel start)
+  int hb[HB_BINS];                // top-k refinement histogram (zeroed at kernel start)
+  int hwave[FNW];                 // its per-wave totals
+  int hsel;                       // the chosen bin, -1 if none reaches k
   int redb[FNW][1];
   double redz[FNW];
 };
@@ -285,13 +289,15 @@ __device__ __forceinline__ void ladder_count(const float (&gm)[R], const int2* p
 }
 
 // Candidate threshold from the ladder (rungs from the slice max down to 1024
-// nats below it, then refinements that split the bracketing interval).
+// nats below it) and, for top-k, one histogram over the bracketing interval.
 //   k > 0 (top-k bound): a threshold with at least k slice elements at or
 //     above it -- the highest rung whose group count reaches k (each counted
-//     group holds at least one such element), refined while the count
-//     exceeds max(1.5 k, 64).  When no rung reaches k (an outlier far above the
-//     rest of the slice), a second round tries 2^11 .. 2^18 below the max;
-//     -inf when that fails too.
+//     group holds at least one such element).  When that count exceeds
+//     max(1.5 k, 64), the bracket between that rung and the one above it is
+//     cut into 1024 bins and the threshold is the edge of the first bin whose
+//     cumulative count reaches k.  When no rung reaches k (an outlier far
+//     above the rest of the slice), a second round tries 2^11 .. 2^18 below
+//     the max; -inf when that fails too.
 //   k <= 0 (top-p alone): the lowest rung whose group count is at most half
 //     the buffer, refined once towards the next rung.
 template <int R>
@@ -321,13 +327,12 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
       }
       if (!found) hi = x[j];
     }
-    int round = 1;
     if (!found) {
       // fewer than k groups within 1024 of the max (an outlier far above the
       // rest): rungs 2^11 .. 2^18 below it
 #pragma unroll
       for (int j = 0; j < RUNGS; ++j) x[j] = ms - (float)(2048 << j);
-      ladder_count<R>(gm, patch, npatch, x, c, round++, sm);
+      ladder_count<R>(gm, patch, npatch, x, c, 1, sm);
 #pragma unroll
       for (int j = 0; j < RUNGS; ++j) {
         if (!found && c[j] >= k) {
@@ -339,26 +344,41 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
       }
       if (!found) return -INFINITY;
     }
-    for (; round < LADDER_ROUNDS && clo > target && hi != INFINITY; ++round) {
-      const float span = hi - lo;
+    if (clo > target && hi != INFINITY) {
+      // one histogram over the bracket [lo, hi): bin g holds the values v
+      // with floor(fl(hi - v) / w) = g (w = (hi - lo) / 1024) that also reach
+      // the bin's lower edge e(g) = fl(hi - (g + 1) w); the counts above hi
+      // are known (fewer than k).  The first bin whose cumulative count
+      // reaches k gives the threshold e(g*); lo stands if none does.
+      const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+      int chi = 0;
 #pragma unroll
-      for (int q = 0; q < RUNGS; ++q) x[q] = hi - span * ((float)(q + 1) / (float)(RUNGS + 1));  // a folded constant, no division
-      ladder_count<R>(gm, patch, npatch, x, c, round, sm);
-      bool f2 = false;
-      float nlo = lo, nhi = hi;
-      int nclo = clo;
-#pragma unroll
-      for (int q = 0; q < RUNGS; ++q) {
-        if (!f2 && c[q] >= k) {
-          f2 = true;
-          nlo = x[q];
-          nclo = c[q];
+      for (int j = 0; j < RUNGS; ++j)
+        if (x[j] == hi) chi = c[j];
+      const float w = (hi - lo) * (1.0f / (float)HB_BINS);
+      const float iw = (float)HB_BINS / (hi - lo);
+      auto add = [&](float v) {
+        if (v < hi && v >= lo) {
+          const int g = max(0, min((int)((hi - v) * iw), HB_BINS - 1));
+          if (v >= hi - (float)(g + 1) * w) atomicAdd(&sm.hb[g], 1);
         }
-        if (!f2) nhi = x[q];
-      }
-      lo = nlo;
-      hi = nhi;
-      clo = nclo;
+      };
+#pragma unroll
+      for (int r = 0; r < R; ++r) add(gm[r]);
+      for (int p = tid; p < npatch; p += FT) add(__int_as_float(patch[p].x));
+      __syncthreads();
+      const uint32_t hc = (uint32_t)sm.hb[tid];
+      const uint32_t incl = wscan_incl_u32(hc);
+      if (lane == 63) sm.hwave[wv] = (int)incl;
+      __syncthreads();
+      uint32_t before = (uint32_t)chi;
+      for (int q = 0; q < wv; ++q) before += (uint32_t)sm.hwave[q];
+      const uint32_t cum = before + incl;
+      if (cum >= (uint32_t)k && cum - hc < (uint32_t)k) sm.hsel = tid;
+      __syncthreads();
+      const int g = sm.hsel;
+      if (g >= 0) lo = hi - (float)(g + 1) * w;
+      return lo;
     }
     return lo;
   }
@@ -454,9 +474,12 @@ __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logi
   }
   float* out = a.out_rows ? a.out_rows + (long long)b * V : nullptr;
   if (tid < LADDER_ROUNDS * RUNGS) (&sm.lad[0][0])[tid] = 0;
+  static_assert(HB_BINS == FT, "one histogram bin per thread");
+  sm.hb[tid] = 0;
   if (tid == 0) {
     sm.cnt = 0;
     sm.npatch = 0;
+    sm.hsel = -1;
   }
 
   // 2. penalties, from the history side, and 3. the group maxima.
@@ -1659,8 +1682,8 @@ struct HostPlan {
   size_t lds;
 };
 
-// Dynamic LDS of the slice kernel at most (its static LDS is under 1 KB).
-constexpr size_t SLICE_LDS_MAX = 160 * 1024 - 1024;
+// Dynamic LDS of the slice kernel at most (its static LDS is under 5 KB).
+constexpr size_t SLICE_LDS_MAX = 160 * 1024 - 6 * 1024;
 
 static HostPlan make_plan(int B, int V, int dtype, int hcap) {
   HostPlan p;
