@@ -1062,21 +1062,6 @@ struct MergeSmem {
   int tok;    // wave 1's draw over the whole list
 };
 
-// Normaliser bounds for the block merge: every thread reads the G summaries
-// itself.
-__device__ __forceinline__ ZBounds z_bounds_loop(const SliceHdr* hd, int G, float m, uint64_t Scand) {
-  ZParts s{0.0, 0.0, 0.0, 0.0, 0};
-  for (int l = 0; l < G; ++l) {
-    const ZParts q = z_slice(hd[l], m);
-    s.lo += q.lo;
-    s.hi += q.hi;
-    s.zl += q.zl;
-    s.zh += q.zh;
-    s.nz += q.nz;
-  }
-  return z_finish(s, Scand);
-}
-
 // Candidates in LDS (any number), filtered by the whole workgroup: masses are
 // block reductions, the top-k cut a histogram-then-rank select, the top-p cut
 // block radix selects.  Every method is called by every thread.
@@ -1435,26 +1420,50 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
 // arguments are read in place from the kernel-argument segment (a pointer,
 // not a copy).  It is inlined: out of line, its LDS pointers arrive as
 // generic pointers and every LDS access becomes a flat access (workload 4
-// took 84.4 us per call that way, 79.2 us inlined).
-__device__ __forceinline__ int merge_block(const SampleKArgs* ap, const FastPlan* pp, int b, RowParams rp, int G, float m,
-                                       float tcov, float ub, char* dyn, ExactSmem* smp) {
+// took 84.4 us per call that way, 79.2 us inlined).  hdl is the kernel's
+// register copy of the summaries (lane s < G holds slice s): the counts and
+// the normaliser bounds come from it, and the candidates are loaded U per
+// thread before any is stored, so a row costs one round trip per U * 512
+// candidates.
+template <int G>
+__device__ __forceinline__ int merge_block(const SampleKArgs* ap, const FastPlan* pp, int b, RowParams rp, const SliceHdr& hdl,
+                                           float m, float tcov, float ub, char* dyn, ExactSmem* smp) {
   const SampleKArgs& a = *ap;
   const FastPlan& P = *pp;
   ExactSmem& sm = *smp;
   const int tid = threadIdx.x, nt = blockDim.x;
-  const SliceHdr* hd = P.hdr + (long long)b * G;
   float* cv = (float*)dyn;
   int* ci = (int*)(dyn + (size_t)G * P.cap * sizeof(float));
-  int N = 0;
-  for (int s = 0; s < G; ++s) {
-    const int ns = hd[s].n;
-    const int2* src = P.cand + ((long long)b * G + s) * P.cap;
-    for (int j = tid; j < ns; j += nt) {
-      const int2 c = src[j];
-      cv[N + j] = __int_as_float(c.x);
-      ci[N + j] = c.y;
+  // slice s's candidates go to [off[s], off[s + 1])
+  int off[G + 1];
+  off[0] = 0;
+#pragma unroll
+  for (int s = 0; s < G; ++s) off[s + 1] = off[s] + min((int)lane_u32((uint32_t)hdl.n, s), P.cap);
+  const int N = off[G];
+  const int2* row = P.cand + (long long)b * G * P.cap;
+  constexpr int U = 8;
+  for (int i0 = 0; i0 < N; i0 += U * nt) {
+    int2 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * nt + tid;
+      int s = 0, os = 0;
+#pragma unroll
+      for (int q = 1; q < G; ++q)
+        if (i >= off[q]) {
+          s = q;
+          os = off[q];
+        }
+      v[u] = row[i < N ? (long long)s * P.cap + (i - os) : 0];
     }
-    N += ns;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * nt + tid;
+      if (i < N) {
+        cv[i] = __int_as_float(v[u].x);
+        ci[i] = v[u].y;
+      }
+    }
   }
   __syncthreads();
   BlockStore st;
@@ -1465,7 +1474,10 @@ __device__ __forceinline__ int merge_block(const SampleKArgs* ap, const FastPlan
   // the normaliser bounds serve the top-p cut alone (rp.use_p is uniform
   // over the workgroup, so the block reductions inside run on every thread)
   ZBounds zb{0ull, 0ull};
-  if (rp.use_p) zb = z_bounds_loop(hd, G, m, st.mass(false, 0.0f));
+  if (rp.use_p) {
+    const uint64_t Scand = st.mass(false, 0.0f);
+    zb = z_finish(z_parts<G>(hdl, (threadIdx.x & 63) < G, m), Scand);
+  }
   if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
   const float invT = rp.invT;
   const double rTc = rp.rTc;
@@ -1665,7 +1677,7 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
     __syncthreads();
     path = s_path;
   } else if (path == 5) {
-    path = merge_block(&merge_kernargs()->a, &merge_kernargs()->p, b, rp, G, m, tcov, ub, dyn, &esm);
+    path = merge_block<G>(&merge_kernargs()->a, &merge_kernargs()->p, b, rp, hd, m, tcov, ub, dyn, &esm);
     if (tid == 0) P.path[b] = path;
     __syncthreads();
   } else if (tid == 0) {
