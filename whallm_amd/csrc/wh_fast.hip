@@ -250,7 +250,7 @@ struct SliceSmem {
   int lad[LADDER_ROUNDS][RUNGS];  // ladder totals per round (zeroed at kernel start)
   int hb[HB_BINS];                // top-k refinement histogram (zeroed at kernel start)
   int hwave[FNW];                 // its per-wave totals
-  int hsel;                       // the chosen bin, -1 if none reaches k
+  int hsel[2];                    // the chosen bins (two uses), -1 if none reaches k
   int redb[FNW][1];
   double redz[FNW];
 };
@@ -288,6 +288,50 @@ __device__ __forceinline__ void ladder_count(const float (&gm)[R], const int2* p
   for (int j = 0; j < RUNGS; ++j) tot[j] = sm.lad[buf][j];
 }
 
+// Top-k cut over an interval: 1024 bins of w = (top - lo) / 1024 over the
+// values v in [lo, top) ([lo, top] when incl); bin g takes the values with
+// floor(fl(top - v) / w) = g that also reach its lower edge
+// e(g) = fl(top - (g + 1) w) (a value the rounding puts one bin too high is
+// not counted, which only lowers the counts).  chi values lie above the
+// interval.  One LDS atomic per value in it, one block scan over the bins
+// (one per thread); the result is the first bin whose cumulative count
+// reaches k, or -1.  The edges do not increase with g, so at least k values
+// are >= e(g*).  The histogram is left zeroed; `slot` picks the LDS word the
+// chosen bin passes through (each use takes its own).
+template <int R>
+__device__ __forceinline__ int hist_cut(const float (&gm)[R], const int2* patch, int npatch, float lo, float top, bool incl,
+                                        int chi, int k, int slot, SliceSmem& sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float w = (top - lo) * (1.0f / (float)HB_BINS);
+  const float iw = (float)HB_BINS / (top - lo);
+  auto add = [&](float v) {
+    if ((v < top || (incl && v == top)) && v >= lo) {
+      const int g = max(0, min((int)((top - v) * iw), HB_BINS - 1));
+      if (v >= top - (float)(g + 1) * w) atomicAdd(&sm.hb[g], 1);
+    }
+  };
+#pragma unroll
+  for (int r = 0; r < R; ++r) add(gm[r]);
+  for (int p = tid; p < npatch; p += FT) add(__int_as_float(patch[p].x));
+  __syncthreads();
+  const uint32_t hc = (uint32_t)sm.hb[tid];
+  sm.hb[tid] = 0;
+  const uint32_t incl_sum = wscan_incl_u32(hc);
+  if (lane == 63) sm.hwave[wv] = (int)incl_sum;
+  __syncthreads();
+  uint32_t before = (uint32_t)chi;
+  for (int q = 0; q < wv; ++q) before += (uint32_t)sm.hwave[q];
+  const uint32_t cum = before + incl_sum;
+  if (cum >= (uint32_t)k && cum - hc < (uint32_t)k) sm.hsel[slot] = tid;
+  __syncthreads();
+  return sm.hsel[slot];
+}
+
+// Width of the interval below the slice max that a small top-k (k <= 64)
+// first tries with one histogram, before the ladder.
+constexpr float TOPK_NEAR = 8.0f;
+constexpr int TOPK_NEAR_K = 64;
+
 // Candidate threshold from the ladder (rungs from the slice max down to 1024
 // nats below it) and, for top-k, one histogram over the bracketing interval.
 //   k > 0 (top-k bound): a threshold with at least k slice elements at or
@@ -307,6 +351,15 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
   // loops with selects), so it stays in registers.
   const float D0[RUNGS] = {0.0f, 0.5f, 1.0f, 2.0f, 4.0f, 16.0f, 128.0f, 1024.0f};
   const int half = cap / 2;
+  if (k > 0 && k <= TOPK_NEAR_K) {
+    // a small k is usually reached within a few nats of the max: one
+    // histogram over [ms - 8, ms] settles it without the ladder
+    const float lo = ms - TOPK_NEAR;
+    if (lo < ms) {
+      const int g = hist_cut<R>(gm, patch, npatch, lo, ms, true, 0, k, 0, sm);
+      if (g >= 0) return ms - (float)(g + 1) * ((ms - lo) * (1.0f / (float)HB_BINS));
+    }
+  }
   float x[RUNGS];
   int c[RUNGS];
 #pragma unroll
@@ -345,39 +398,14 @@ __device__ __forceinline__ float ladder_tau(const float (&gm)[R], const int2* pa
       if (!found) return -INFINITY;
     }
     if (clo > target && hi != INFINITY) {
-      // one histogram over the bracket [lo, hi): bin g holds the values v
-      // with floor(fl(hi - v) / w) = g (w = (hi - lo) / 1024) that also reach
-      // the bin's lower edge e(g) = fl(hi - (g + 1) w); the counts above hi
-      // are known (fewer than k).  The first bin whose cumulative count
-      // reaches k gives the threshold e(g*); lo stands if none does.
-      const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+      // one histogram over the bracket [lo, hi); the counts above hi are
+      // known (fewer than k), and lo stands if no bin reaches k
       int chi = 0;
 #pragma unroll
       for (int j = 0; j < RUNGS; ++j)
         if (x[j] == hi) chi = c[j];
-      const float w = (hi - lo) * (1.0f / (float)HB_BINS);
-      const float iw = (float)HB_BINS / (hi - lo);
-      auto add = [&](float v) {
-        if (v < hi && v >= lo) {
-          const int g = max(0, min((int)((hi - v) * iw), HB_BINS - 1));
-          if (v >= hi - (float)(g + 1) * w) atomicAdd(&sm.hb[g], 1);
-        }
-      };
-#pragma unroll
-      for (int r = 0; r < R; ++r) add(gm[r]);
-      for (int p = tid; p < npatch; p += FT) add(__int_as_float(patch[p].x));
-      __syncthreads();
-      const uint32_t hc = (uint32_t)sm.hb[tid];
-      const uint32_t incl = wscan_incl_u32(hc);
-      if (lane == 63) sm.hwave[wv] = (int)incl;
-      __syncthreads();
-      uint32_t before = (uint32_t)chi;
-      for (int q = 0; q < wv; ++q) before += (uint32_t)sm.hwave[q];
-      const uint32_t cum = before + incl;
-      if (cum >= (uint32_t)k && cum - hc < (uint32_t)k) sm.hsel = tid;
-      __syncthreads();
-      const int g = sm.hsel;
-      if (g >= 0) lo = hi - (float)(g + 1) * w;
+      const int g = hist_cut<R>(gm, patch, npatch, lo, hi, false, chi, k, 1, sm);
+      if (g >= 0) lo = hi - (float)(g + 1) * ((hi - lo) * (1.0f / (float)HB_BINS));
       return lo;
     }
     return lo;
@@ -479,7 +507,8 @@ __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logi
   if (tid == 0) {
     sm.cnt = 0;
     sm.npatch = 0;
-    sm.hsel = -1;
+    sm.hsel[0] = -1;
+    sm.hsel[1] = -1;
   }
 
   // 2. penalties, from the history side, and 3. the group maxima.
