@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--engine", choices=["auto", "exact"], default="auto",
+                    help="sample workloads: 'exact' times the one-workgroup-per-row exact engine (no workspace)")
     ap.add_argument("--lmhead", metavar="M,K,V", default=None,
                     help="time the LM head (wh_lmhead_logits and wh_lmhead_greedy) at this shape instead")
     ap.add_argument("--summarize-profile", metavar="OUT", default=None,
@@ -463,19 +465,22 @@ def main():
     u = torch.from_numpy(w.uniforms).to(dev)
 
     # Parity on set 0 before timing.
-    tok0 = sampling.sample(sets[0][0], history=sets[0][1], history_len=hl, uniforms=u, top_k_rows=kr, **prm)
+    tok0 = sampling.sample(sets[0][0], history=sets[0][1], history_len=hl, uniforms=u, top_k_rows=kr,
+                           engine=args.engine, **prm)
     p = synth.oracle_params(w, o.make_params)
     want, _ = o.sample(w.logits_f32, p, w.uniforms, w.history, w.history_len)
     faithful, _ = o.sample_faithful(w.logits_f32, p, w.uniforms, w.history, w.history_len)
     got = tok0.cpu().numpy()
-    paths = sampling.last_paths(dev, w.B).cpu().numpy()
     parity = {"rows": int(w.B), "contract_bit_exact": bool(np.array_equal(got, want)),
-              "faithful_float32_agreement": float(np.mean(got == faithful)),
-              "rows_exact_fallback": int(np.sum((paths == 1) | (paths == 3)))}
+              "faithful_float32_agreement": float(np.mean(got == faithful))}
+    if args.engine == "auto":
+        paths = sampling.last_paths(dev, w.B).cpu().numpy()
+        parity["rows_exact_fallback"] = int(np.sum((paths == 1) | (paths == 3)))
 
     # The timed loop calls the C ABI through pre-bound argument structs (one
     # per input set), as a decode loop that refills its buffers would.
-    calls = [sampling.SampleCall(x, history=h, history_len=hl, uniforms=u, top_k_rows=kr, **prm) for x, h in sets]
+    calls = [sampling.SampleCall(x, history=h, history_len=hl, uniforms=u, top_k_rows=kr, engine=args.engine, **prm)
+             for x, h in sets]
     for i in range(args.warmup):
         calls[i % len(calls)]()
     torch.cuda.synchronize()
@@ -496,7 +501,8 @@ def main():
     parity["timed_set0_tokens_bit_exact"] = bool(np.array_equal(tok_set0, want))
     nbytes = w.bytes_per_call()
     achieved = nbytes / avg_s / 1e9
-    traffic, traffic_src = measured_traffic(args.workload, w.name)
+    # the committed traffic records are the default (fast / wide) engine's
+    traffic, traffic_src = measured_traffic(args.workload, w.name) if args.engine == "auto" else (None, None)
     res = {
         "metric": METRIC,
         "value": w.B * args.steps / wall,
@@ -515,11 +521,14 @@ def main():
                    "input_sets": len(sets), "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
-                     "kernel": "wh_sample (slice_kernel + merge_kernel)",
+                     "kernel": ("wh_sample (slice_kernel + merge_kernel)" if args.engine == "auto"
+                                else "wh_sample exact engine (sample_exact_kernel)"),
                      "kernel_avg_us": avg_s * 1e6, "algorithmic_bytes": nbytes,
                      "traffic_source": traffic_src},
         "parity": parity,
     }
+    if args.engine != "auto":
+        res["config"]["engine"] = args.engine
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(res))
