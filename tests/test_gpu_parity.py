@@ -409,3 +409,30 @@ def test_verify_fused_random(S, dev, oracle, seed):
                           T, uniforms=torch.from_numpy(u).to(dev))
     assert np.array_equal(a.cpu().numpy(), oa)
     assert np.array_equal(t.cpu().numpy(), ot)
+
+
+@pytest.mark.parametrize("chain", [0, 1])
+def test_confident_rows_settle_on_fast_engine(S, dev, oracle, chain):
+    """Rows where one token holds most of the mass (a confident model), with
+    top-p and min-p together: min-p sets the slices' thresholds, so the
+    slices take no float sums and the candidates' normaliser bounds cannot
+    place the top-p cut.  The merge's second pass (a float sum over the row)
+    must settle every row on the fast engine (path 7 or 8, no exact-engine
+    fallback), with tokens and kept sizes equal to the oracle's."""
+    rng = np.random.default_rng(1300 + chain)
+    B, V = 32, 151936
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    lead = rng.integers(0, V, B)
+    x[np.arange(B), lead] += np.float32(12.0) + rng.uniform(0.0, 6.0, B).astype(np.float32)
+    u = rng.random(B, dtype=np.float32)
+    c = (dict(temperature=1.0, top_p=0.9, top_k=0, min_p=0.05) if chain == 0
+         else dict(temperature=0.7, top_p=0.95, top_k=20, min_p=0.01))
+    p = oracle.make_params(B, chain=chain, **c)
+    ot, ok = oracle.sample(x, p, u)
+    announce(f"wh_sample confident rows chain={chain} {c}")
+    tok, kept = S.sample(torch.from_numpy(x).to(dev), uniforms=torch.from_numpy(u).to(dev), return_kept=True,
+                         chain=chain, **c)
+    paths = S.last_paths(dev, B).cpu().numpy()
+    assert np.array_equal(kept.cpu().numpy(), ok)
+    assert np.array_equal(tok.cpu().numpy(), ot)
+    assert not np.any((paths == 1) | (paths == 3)), paths

@@ -90,8 +90,11 @@ struct FastPlan {
   int rule_cap;    // largest k a slice may bound
   int pcap;        // capacity of the penalised-element list (with penalties)
   int codes_bytes; // LDS bytes of the penalty codes (0 without penalties)
+  int zpass;       // the merge may take a row's float sum when its bounds leave a top-p cut open:
+                   // bit 0 for the register merge, bit 1 for the block merge (LDS permitting)
   int* path;       // [B] 0: merged in registers, 4: merged through LDS, 1: exact engine
-                   //     (overflow / no bound), 2: greedy, 3: exact engine (top-p cut unsettled)
+                   //     (overflow / no bound), 2: greedy, 3: exact engine (top-p cut unsettled),
+                   //     7 / 8: merged in registers / through LDS after the row's float sum
   SliceHdr* hdr;   // [B * G]
   int2* cand;      // [B * G * cap] (value bits, id), in no particular order
 };
@@ -831,7 +834,9 @@ struct ZBounds {
 //  * Lower bound: the candidates' exact masses, plus for every group counted
 //    in a band [t_j, t_(j-1)) at least one element of mass
 //    >= floor(2^44 e^(t_j - m) (1 - eps)) - 1.
-//  * Upper bound: every non-candidate is below tau.
+//  * Upper bound: every non-candidate is below tau.  (A row whose
+//    candidates hold most but not all of the mass can leave a top-p cut
+//    open this way; rescue_row then takes a float sum over the row.)
 //  * When every slice carries its float sum zf (hardware exp, relative error
 //    far below eps = 2e-4 for every term that exp_fix44 does not flush to 0),
 //    both bounds are also taken from zf.
@@ -1089,6 +1094,7 @@ struct MergeSmem {
   ZParts zp;  // the summaries' share of the normaliser bounds
   int n;      // hot candidates listed
   int tok;    // wave 1's draw over the whole list
+  uint64_t sv[5];  // [3], [4]: the normaliser bounds of a row whose top-p cut they left open
 };
 
 // Candidates in LDS (any number), filtered by the whole workgroup: masses are
@@ -1444,6 +1450,74 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
   return 0;
 }
 
+// Normaliser bounds narrowed by a float sum zs of exp(l - m) over a row of V
+// values (relative error far below EPS, each term's floor costs under 1).
+__device__ __forceinline__ void tighten_z(ZBounds& zb, double zs, int V) {
+  const double SC = 17592186044416.0, EPS = 2e-4, LIM = 4.0e18;
+  const double zl = zs * SC * (1.0 - EPS) - (double)V, zh = zs * SC * (1.0 + EPS) + (double)V;
+  const uint64_t lo = zl <= 0.0 ? 0ull : (uint64_t)zl;
+  const uint64_t hi = zh >= LIM ? (1ull << 62) : (uint64_t)ceil(zh);
+  zb.lo = lo > zb.lo ? lo : zb.lo;
+  zb.hi = hi < zb.hi ? hi : zb.hi;
+}
+
+// The filters and the draw of a listed row by wave 0 (path 0, or 3 for the
+// exact engine): the quick decision from the totals when min-p is the last
+// filter and there is no top-k, else the register merge.  Either way wave 0
+// takes part in exactly one workgroup barrier, after which wave 1's
+// speculative token is in sm.tok.
+__device__ __forceinline__ int merge_filters(const SampleKArgs& a, int b, const RowParams& rp, float m, float tcov, float ub,
+                                             const HotList& hl, int N, uint64_t m_all, uint64_t m_cov, uint64_t ZV,
+                                             ZBounds zb, MergeSmem& sm) {
+  const int lane = threadIdx.x & 63;
+  // with min-p last and no top-k the totals settle most rows: then the
+  // candidates need not be loaded at all
+  const int quick = (rp.use_m && !rp.use_k && !a.out_rows) ? quick_filters(rp, zb, m_cov) : -1;
+  if (quick >= 0) {
+    __syncthreads();  // wave 1's speculative token is in sm.tok
+    if (quick == 0 && lane == 0) {
+      if (a.tokens) a.tokens[b] = ZV ? sm.tok : 0;
+      if (a.kept) a.kept[b] = N;
+    }
+    return quick;
+  }
+  if (N <= 64) return merge_regs<1>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+  if (N <= 128) return merge_regs<2>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+  if (N <= 256) return merge_regs<4>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+  if (N <= 512) return merge_regs<8>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+  return merge_regs<QM>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+}
+
+// The filters and the draw over candidates in LDS (src), run by every thread
+// of the workgroup: path 4 done, 3 when the bounds zb leave a top-p cut open.
+__device__ __forceinline__ int block_finish(const SampleKArgs& a, int b, const RowParams& rp, float m, float tcov, float ub,
+                                            const CandSource& src0, ZBounds zb, ExactSmem& sm) {
+  const int tid = threadIdx.x;
+  BlockStore st{src0, Pred{0, 0, 0, 0, 0, 0, 0.0f, -INFINITY}, m, &sm};
+  if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
+  const float invT = rp.invT;
+  const double rTc = rp.rTc;
+  const Pred pr = st.pr;
+  const CandSource src = st.src;
+  auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, rTc)); };
+  // the draw weights' sum, the kept count and the draw in one pass plus the
+  // target's bin
+  uint64_t ZV;
+  int nkept;
+  const int tok = block_draw_id(src, pr, vw, ub, a.tokens != nullptr, sm, &ZV, &nkept);
+  if (tid == 0 && a.tokens) a.tokens[b] = tok;
+  if (tid == 0 && a.kept) a.kept[b] = nkept;
+  float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
+  if (out) {
+    const double lz = log(ldexp((double)ZV, -44));
+    src.each([&](int i, float l) {
+      if (!pr.keep(i, l)) return;
+      out[i] = a.out_mode == WH_OUT_MASKED ? l : (float)((double)chain_scale(a.chain, l - m, invT, rTc) - lz);
+    });
+  }
+  return 4;
+}
+
 // Block merge of row b (any number of candidates), run by every thread of
 // the workgroup.  Returns the path code (4 done, 3 exact engine).  The
 // arguments are read in place from the kernel-argument segment (a pointer,
@@ -1456,7 +1530,7 @@ __device__ __forceinline__ int merge_regs(const SampleKArgs& a, int b, const Row
 // candidates.
 template <int G>
 __device__ __forceinline__ int merge_block(const SampleKArgs* ap, const FastPlan* pp, int b, RowParams rp, const SliceHdr& hdl,
-                                           float m, float tcov, float ub, char* dyn, ExactSmem* smp) {
+                                           float m, float tcov, float ub, char* dyn, ExactSmem* smp, MergeSmem* msp) {
   const SampleKArgs& a = *ap;
   const FastPlan& P = *pp;
   ExactSmem& sm = *smp;
@@ -1495,40 +1569,71 @@ __device__ __forceinline__ int merge_block(const SampleKArgs* ap, const FastPlan
     }
   }
   __syncthreads();
-  BlockStore st;
-  st.src = CandSource{cv, ci, N};
-  st.pr = Pred{0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
-  st.m = m;
-  st.sm = &sm;
   // the normaliser bounds serve the top-p cut alone (rp.use_p is uniform
   // over the workgroup, so the block reductions inside run on every thread)
+  const CandSource src{cv, ci, N};
   ZBounds zb{0ull, 0ull};
   if (rp.use_p) {
-    const uint64_t Scand = st.mass(false, 0.0f);
-    zb = z_finish(z_parts<G>(hdl, (threadIdx.x & 63) < G, m), Scand);
+    BlockStore st{src, Pred{0, 0, 0, 0, 0, 0, 0.0f, -INFINITY}, m, &sm};
+    zb = z_finish(z_parts<G>(hdl, (threadIdx.x & 63) < G, m), st.mass(false, 0.0f));
   }
-  if (!run_filters(st, a, rp, m, tcov, zb)) return 3;
-  const float invT = rp.invT;
-  const double rTc = rp.rTc;
-  const Pred pr = st.pr;
-  const CandSource src = st.src;
-  auto vw = [&](int, float l) { return exp_fix44(chain_scale(a.chain, l - m, invT, rTc)); };
-  // the draw weights' sum, the kept count and the draw in one pass plus the
-  // target's bin
-  uint64_t ZV;
-  int nkept;
-  const int tok = block_draw_id(src, pr, vw, ub, a.tokens != nullptr, sm, &ZV, &nkept);
-  if (tid == 0 && a.tokens) a.tokens[b] = tok;
-  if (tid == 0 && a.kept) a.kept[b] = nkept;
-  float* out = a.out_rows ? a.out_rows + (long long)b * a.V : nullptr;
-  if (out) {
-    const double lz = log(ldexp((double)ZV, -44));
-    src.each([&](int i, float l) {
-      if (!pr.keep(i, l)) return;
-      out[i] = a.out_mode == WH_OUT_MASKED ? l : (float)((double)chain_scale(a.chain, l - m, invT, rTc) - lz);
-    });
+  const int path = block_finish(a, b, rp, m, tcov, ub, src, zb, sm);
+  if (path == 3 && tid == 0) {
+    // for the second bounds pass (rescue_row)
+    msp->n = N;
+    msp->sv[3] = zb.lo;
+    msp->sv[4] = zb.hi;
   }
-  return 4;
+  return path;
+}
+
+// A second bounds pass for a row whose bounds left the top-p cut open
+// (typically a row whose candidates hold most but not all of the mass, with
+// min-p setting the slices' thresholds, so the slices took no float sums):
+// one float sum of exp(l - m) over the row bounds Z to 2e-4, and the filters
+// run again, through the block merge, on the candidates still in LDS -- the
+// register merge's hot list (from_list; moved into value / id arrays
+// first) or the block merge's arrays.  The penalty table goes after them.
+// Returns 7 or 8 (settled after the register or the block merge) or 3 (the
+// exact engine).  Out of line and called at the end of the merge kernel,
+// where nothing of the caller's is live: inlined or called earlier it cost
+// the common path registers (2-5 us per call); its LDS accesses are flat
+// accesses.  Every thread of the workgroup calls it.
+__device__ __noinline__ int rescue_row(const SampleKArgs* ap, const FastPlan* pp, int b, float m, float tcov, float ub,
+                                       char* dyn, ExactSmem* esm, MergeSmem* msm, int G, int from_list) {
+  const SampleKArgs& a = *ap;
+  const FastPlan& P = *pp;
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const RowParams rp = row_params(a, row_raw(a, a, b), P.rule_cap);
+  const int N = msm->n;
+  float* cv = (float*)dyn;
+  int* ci;
+  char* pen;
+  if (from_list) {
+    // the hot list (at most QSPEC * 64 entries) into value / id arrays in
+    // place: every entry is read before any is written
+    constexpr int LPT = (QSPEC * 64) / (MW * 64);
+    const HotList hl = hot_list(dyn);
+    int2 e[LPT];
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) e[q] = hl.cand[min(tid + q * nt, N > 0 ? N - 1 : 0)];
+    __syncthreads();
+    ci = (int*)(dyn + (size_t)QSPEC * 64 * sizeof(float));
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+      if (tid + q * nt < N) {
+        cv[tid + q * nt] = __int_as_float(e[q].x);
+        ci[tid + q * nt] = e[q].y;
+      }
+    pen = dyn + (size_t)QSPEC * 64 * 8;
+  } else {
+    ci = (int*)(dyn + (size_t)G * P.cap * sizeof(float));
+    pen = dyn + (size_t)G * P.cap * 8;
+  }
+  ZBounds zb{msm->sv[3], msm->sv[4]};
+  tighten_z(zb, a.dtype == WH_DTYPE_BF16 ? row_zsum_t<1>(a, b, m, pen, *esm) : row_zsum_t<0>(a, b, m, pen, *esm), a.V);
+  const int path = block_finish(a, b, rp, m, tcov, ub, CandSource{cv, ci, N}, zb, *esm);
+  return path == 3 ? 3 : (from_list ? 7 : 8);
 }
 
 template <int G>
@@ -1577,6 +1682,7 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
   // the path is the same in every wave: 0 register merge, 1 exact engine,
   // 2 greedy, 5 block merge (too many candidates for the loaded chunks)
   int path;
+  int from_list = 1;  // a path 3 row came from the register merge (0: the block merge)
   if (rp.greedy) path = flagged ? 1 : 2;
   else if (flagged || rp.all) path = 1;
   else path = G * ((nmax + 63) / 64) <= QSPEC ? 0 : 5;
@@ -1683,22 +1789,13 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
       totals4(sm.acc, tot);
       const uint64_t m_all = tot[0], m_cov = tot[1], ZV = tot[3];
       const ZBounds zb = z_finish(sm.zp, m_all + tot[2]);
-      // with min-p last and no top-k the totals settle most rows: then the
-      // candidates need not be loaded at all
-      const int quick = (rp.use_m && !rp.use_k && !a.out_rows) ? quick_filters(rp, zb, m_cov) : -1;
-      if (quick >= 0) {
-        __syncthreads();  // wave 1's speculative token is in sm.tok
-        path = quick;
-        if (quick == 0 && lane == 0) {
-          if (a.tokens) a.tokens[b] = ZV ? sm.tok : 0;
-          if (a.kept) a.kept[b] = N;
-        }
-      } else if (N <= 64) path = merge_regs<1>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
-      else if (N <= 128) path = merge_regs<2>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
-      else if (N <= 256) path = merge_regs<4>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
-      else if (N <= 512) path = merge_regs<8>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
-      else path = merge_regs<QM>(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
+      path = merge_filters(a, b, rp, m, tcov, ub, hl, N, m_all, m_cov, ZV, zb, sm);
       if (lane == 0) {
+        if (path == 3) {
+          // for the second bounds pass (rescue_row)
+          sm.sv[3] = zb.lo;
+          sm.sv[4] = zb.hi;
+        }
         s_path = path;
         P.path[b] = path;
       }
@@ -1706,11 +1803,17 @@ __global__ void __launch_bounds__(MW * 64) merge_kernel(const SliceHdr* __restri
     __syncthreads();
     path = s_path;
   } else if (path == 5) {
-    path = merge_block<G>(&merge_kernargs()->a, &merge_kernargs()->p, b, rp, hd, m, tcov, ub, dyn, &esm);
+    from_list = 0;
+    path = merge_block<G>(&merge_kernargs()->a, &merge_kernargs()->p, b, rp, hd, m, tcov, ub, dyn, &esm, &sm);
     if (tid == 0) P.path[b] = path;
     __syncthreads();
   } else if (tid == 0) {
     P.path[b] = path;
+  }
+  if (path == 3 && rp.use_p && (P.zpass & (from_list ? 1 : 2))) {
+    path = rescue_row(&merge_kernargs()->a, &merge_kernargs()->p, b, m, tcov, ub, dyn, &esm, &sm, G, from_list);
+    if (tid == 0) P.path[b] = path;
+    __syncthreads();
   }
   if (path == 1 || path == 3) exact_row(merge_kernargs()->a, b, dyn, esm);
 }
@@ -1723,6 +1826,8 @@ struct HostPlan {
   size_t lds;
 };
 
+// Dynamic LDS of the merge kernel at most (its static LDS is under 13 KB).
+constexpr size_t MERGE_LDS_MAX = 160 * 1024 - 16 * 1024;
 // Dynamic LDS of the slice kernel at most (its static LDS is under 5 KB).
 constexpr size_t SLICE_LDS_MAX = 160 * 1024 - 6 * 1024;
 
@@ -1863,7 +1968,13 @@ int launch_sample(const SampleKArgs& k0, const wh_sample_args* p, hipStream_t st
   fp.path = (int*)(ws + wl.path);
   fp.hdr = (SliceHdr*)(ws + wl.hdr);
   fp.cand = (int2*)(ws + wl.cand);
-  const size_t lds_merge = std::max({(size_t)hp.G * hp.cap * 8, penalty_lds_bytes(k), HOT_LIST_BYTES});
+  // the list stays in place under the penalty table of a second bounds pass,
+  // when both fit the LDS next to the merge kernel's static arrays
+  const size_t pen = penalty_lds_bytes(k), blk = (size_t)hp.G * hp.cap * 8;
+  const size_t lst = (size_t)QSPEC * 64 * 8;  // the hot list as value / id arrays
+  fp.zpass = (lst + pen <= MERGE_LDS_MAX ? 1 : 0) | (blk + pen <= MERGE_LDS_MAX ? 2 : 0);
+  const size_t lds_merge =
+      std::max({blk, pen, HOT_LIST_BYTES, (fp.zpass & 1) ? lst + pen : 0, (fp.zpass & 2) ? blk + pen : 0});
   int rc = launch_slice(k.dtype, hp.R, k, fp, hp.lds, st);
   if (rc) return rc;
   hipError_t e = hipGetLastError();

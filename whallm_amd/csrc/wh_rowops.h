@@ -550,6 +550,40 @@ __device__ __forceinline__ void exact_row_impl(const SampleKArgs& a, int b, char
   }
 }
 
+// A float sum of exp(l - m) over row b's penalised values with the hardware
+// exponential, for normaliser bounds when the candidates' own bounds cannot
+// settle a top-p cut.  Each thread sums fewer than 2^10 terms in float32 and
+// the threads' sums are added in double, so the relative error stays far
+// below the 2e-4 the bounds allow, for every term exp_fix44 does not flush
+// to 0 (the same argument as the slice sums).  The row is read as 16-byte
+// groups (the fast engine's rows are aligned and V a multiple of the group);
+// the penalty table goes to dyn.  Every thread of the workgroup calls it.
+template <int DT>
+__device__ __forceinline__ double row_zsum_t(const SampleKArgs& a, int b, float m, char* dyn, ExactSmem& sm) {
+  const int tid = threadIdx.x, nt = blockDim.x, V = a.V;
+  constexpr int EPT = DT ? 8 : 4;
+  RowCtx rc;
+  rc.V = V;
+  rc.xf = DT ? nullptr : (const float*)a.logits + b * a.row_stride;
+  rc.xb = DT ? (const uint16_t*)a.logits + b * a.row_stride : nullptr;
+  rc.hmask = -1;
+  if (a.hcap > 0) build_penalties(a, b, rc, dyn, 0, V);
+  const uint4* row = DT ? (const uint4*)rc.xb : (const uint4*)rc.xf;
+  float z = 0.0f;
+  if (m != -INFINITY) {
+    for (int g = tid; g < V / EPT; g += nt) {
+      const uint4 q = row[g];
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const uint32_t w = e / (EPT / 4) == 0 ? q.x : e / (EPT / 4) == 1 ? q.y : e / (EPT / 4) == 2 ? q.z : q.w;
+        const float r = DT ? __uint_as_float((e & 1) ? (w & 0xFFFF0000u) : (w << 16)) : __uint_as_float(w);
+        z += __expf(rc.val_from(g * EPT + e, r) - m);
+      }
+    }
+  }
+  return block_reduce((double)z, (double*)sm.scratch64, OpSumF64(), 0.0);
+}
+
 __device__ __noinline__ void exact_row(const SampleKArgs& a, int b, char* dyn_smem, ExactSmem& sm) {
   exact_row_impl(a, b, dyn_smem, sm);
 }

@@ -250,7 +250,9 @@ def last_paths(device, B: int) -> torch.Tensor:
     """Per-row engine path of the last workspace call on the current
     stream: 0 merged from candidates, 1 exact engine (candidate or list
     overflow), 2 greedy, 3 exact engine (top-p cut not settled by the
-    normaliser bounds), 6 wide exact engine (top-p alone or no filter).
+    normaliser bounds), 4 merged from candidates through LDS (large sets),
+    6 wide exact engine (top-p alone or no filter), 7 merged from candidates
+    after a float sum over the row settled the top-p cut.
     Diagnostics only: results are identical."""
     ws = L.workspace(torch.device(device), 0)
     return ws[:4 * B].view(torch.int32).clone()
