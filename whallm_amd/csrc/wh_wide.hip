@@ -115,15 +115,33 @@ __device__ __forceinline__ void wx_pen_table(const SampleKArgs& a, int b, int lo
   }
 }
 
-// A thread's E raw entries of the slice, ids lo + tid + 256 j (coalesced),
-// every load issued before any is used; entries past hi are never read.
+// A thread's E raw entries of the slice, ids lo + tid + 256 j (coalesced).
+// Every load is unconditional, from an in-bounds address (entries past hi
+// read entry lo and become 0), with the element type chosen once outside
+// the loop: the E loads then issue back to back and are waited for once.
+// (Conditional loads had compiled to one branch and one full wait per
+// entry, E dependent round trips per thread in every step of the engine.)
 template <int E>
 __device__ __forceinline__ void wx_raw(const RowCtx& rc, int lo, int hi, float (&v)[E]) {
+  if (rc.xf) {
 #pragma unroll
-  for (int j = 0; j < E; ++j) {
-    const int i = lo + threadIdx.x + WX_T * j;
-    v[j] = i < hi ? rc.raw(i) : 0.0f;
+    for (int j = 0; j < E; ++j) {
+      const int i = lo + threadIdx.x + WX_T * j;
+      v[j] = rc.xf[i < hi ? i : lo];
+    }
+  } else {
+    uint16_t h[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+      const int i = lo + threadIdx.x + WX_T * j;
+      h[j] = rc.xb[i < hi ? i : lo];
+    }
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] = bf16_to_f32(h[j]);
   }
+#pragma unroll
+  for (int j = 0; j < E; ++j)
+    if (lo + (int)threadIdx.x + WX_T * j >= hi) v[j] = 0.0f;
 }
 // Raw entries to effective (penalised, -0 as +0) values.
 template <int E>
