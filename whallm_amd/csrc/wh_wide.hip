@@ -143,6 +143,25 @@ __device__ __forceinline__ void wx_raw(const RowCtx& rc, int lo, int hi, float (
   for (int j = 0; j < E; ++j)
     if (lo + (int)threadIdx.x + WX_T * j >= hi) v[j] = 0.0f;
 }
+// A thread's E consecutive raw entries s0 .. s0 + E - 1 (the pick step's
+// layout), loaded the same way: unconditional, in bounds, back to back.
+template <int E>
+__device__ __forceinline__ void wx_raw_run(const RowCtx& rc, int s0, int hi, float (&v)[E]) {
+  const int last = hi - 1;  // the slice is never empty
+  if (rc.xf) {
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] = rc.xf[min(s0 + j, last)];
+  } else {
+    uint16_t h[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) h[j] = rc.xb[min(s0 + j, last)];
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] = bf16_to_f32(h[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < E; ++j)
+    if (s0 + j >= hi) v[j] = 0.0f;
+}
 // Raw entries to effective (penalised, -0 as +0) values.
 template <int E>
 __device__ __forceinline__ void wx_pen(const RowCtx& rc, int lo, int hi, float (&v)[E]) {
@@ -553,8 +572,7 @@ __global__ void __launch_bounds__(WX_T) wx_pick_kernel(SampleKArgs a, WxPtrs P) 
   // E consecutive ids per thread, so the block scan runs in id order
   const int s0 = lo + tid * E;
   float v[E];
-#pragma unroll
-  for (int j = 0; j < E; ++j) v[j] = s0 + j < hi ? rc.raw(s0 + j) : 0.0f;
+  wx_raw_run<E>(rc, s0, hi, v);
   wx_pen_table(a, b, lo, hi, dyn, rc);
 #pragma unroll
   for (int j = 0; j < E; ++j) v[j] = s0 + j < hi ? rc.val_from(s0 + j, v[j]) : 0.0f;
