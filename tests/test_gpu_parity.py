@@ -436,3 +436,42 @@ def test_confident_rows_settle_on_fast_engine(S, dev, oracle, chain):
     assert np.array_equal(kept.cpu().numpy(), ok)
     assert np.array_equal(tok.cpu().numpy(), ot)
     assert not np.any((paths == 1) | (paths == 3)), paths
+    assert np.any((paths == 7) | (paths == 8)), paths  # the second pass ran
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_confident_rows_with_penalties_settle(S, dev, oracle, dtype):
+    """The merge's second bounds pass with a penalty table (built after the
+    candidates in LDS): confident bf16 and float32 rows, penalties over a
+    history that holds the leading token in half the rows, Whallm's order
+    with top-p, min-p and top-k.  Tokens and kept sizes equal to the oracle's,
+    no exact-engine fallback."""
+    from whallm_amd import synth
+
+    rng = np.random.default_rng(1400 + (dtype == "bf16"))
+    B, V, H = 32, 151936, 256
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    lead = rng.integers(0, V, B)
+    x[np.arange(B), lead] += np.float32(12.0) + rng.uniform(0.0, 6.0, B).astype(np.float32)
+    hist = rng.integers(0, V, (B, H)).astype(np.int32)
+    hist[::2, :8] = lead[::2, None]
+    hl = np.full(B, H, np.int32)
+    if dtype == "bf16":
+        bits = synth.f32_to_bf16_bits(x)
+        x = synth.bf16_bits_to_f32(bits)
+        xd = torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        xd = torch.from_numpy(x).to(dev)
+    u = rng.random(B, dtype=np.float32)
+    c = dict(temperature=0.8, top_p=0.95, top_k=40, min_p=0.01, repetition_penalty=1.2, presence_penalty=0.3,
+             frequency_penalty=0.1, repetition_context=H, presence_context=H, frequency_context=H)
+    p = oracle.make_params(B, chain=1, **c)
+    ot, ok = oracle.sample(x, p, u, hist, hl)
+    announce(f"wh_sample confident rows with penalties {dtype}")
+    tok, kept = S.sample(xd, uniforms=torch.from_numpy(u).to(dev), history=torch.from_numpy(hist).to(dev),
+                         history_len=torch.from_numpy(hl).to(dev), return_kept=True, chain=1, **c)
+    paths = S.last_paths(dev, B).cpu().numpy()
+    assert np.array_equal(kept.cpu().numpy(), ok)
+    assert np.array_equal(tok.cpu().numpy(), ot)
+    assert not np.any((paths == 1) | (paths == 3)), paths
+    assert np.any((paths == 7) | (paths == 8)), paths  # the second pass ran
