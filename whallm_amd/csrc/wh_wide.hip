@@ -44,7 +44,8 @@ namespace wh {
 constexpr int WX_T = 256;       // threads per slice workgroup
 constexpr int WX_BINS = 2048;   // mass bins, 1/64 nat each, below the row max
 constexpr int WX_CAP = 8192;    // boundary-bin list capacity per row
-constexpr int WX_RANK = 1024;   // lists up to this long are ranked directly
+constexpr int WX_RANK = 1024;   // sub-bin lists up to this long are ranked directly
+constexpr int WX_DIRECT = 64;   // boundary lists up to this long are ranked without sub-bins
 constexpr int WX_MAXG = 256;    // slices per row, at most (V <= 2^18, 1024-entry slices)
 constexpr int WX_DONE = 1;      // WxRec.flags: token, count and row already written
 constexpr int WX_NONE = 2;      // WxRec.flags: nothing kept (set by the collect step)
@@ -445,7 +446,7 @@ __global__ void __launch_bounds__(1024) wx_resolve_kernel(SampleKArgs a, WxPtrs 
   const float m = wx_row_max(P, b, sf);
   const uint64_t target = r.R - r.cum_excl;  // 0 < target <= the list's mass
   uint64_t cstar = 0;
-  if (n <= WX_RANK) {
+  if (n <= WX_DIRECT) {
     // each listed element's inclusive mass in (value desc, id desc) order,
     // summed over every other from broadcast reads (composites unique)
     uint64_t* lc = (uint64_t*)dyn;
@@ -467,16 +468,94 @@ __global__ void __launch_bounds__(1024) wx_resolve_kernel(SampleKArgs a, WxPtrs 
     __syncthreads();
     cstar = esm.bcast64[0];
   } else {
-    float* lv = (float*)dyn;
-    int* li = (int*)(dyn + WX_CAP * sizeof(float));
-    for (int j = tid; j < n; j += blockDim.x) {
-      lv[j] = P.list_v[(size_t)b * WX_CAP + j];
-      li[j] = P.list_i[(size_t)b * WX_CAP + j];
+    // 256 sub-bins of the boundary bin (monotone in the value, equal values
+    // alike): one pass of masses, a scan for the sub-bin where the target
+    // falls, and the broadcast ranking over that sub-bin's entries (the
+    // ranking costs n^2 broadcast reads: 13 us for a list of 1024); a
+    // sub-bin of more than WX_RANK entries takes the radix select over the
+    // whole list
+    uint64_t* sub = (uint64_t*)dyn;
+    uint64_t* lc = sub + 256;
+    uint64_t* lw = lc + WX_RANK;
+    __shared__ int s_cnt, s_star;
+    __shared__ uint64_t s_rem;
+    if (tid < 256) sub[tid] = 0;
+    if (tid == 0) s_cnt = 0;
+    __syncthreads();
+    constexpr int LPT = WX_CAP / 1024;  // entries per thread at most
+    float lv[LPT];
+    int li[LPT], sb[LPT];
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const int j = tid + q * 1024;
+      lv[q] = P.list_v[(size_t)b * WX_CAP + (j < n ? j : 0)];
+      li[q] = P.list_i[(size_t)b * WX_CAP + (j < n ? j : 0)];
+    }
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      const float d = (m - lv[q]) * 64.0f - (float)r.bstar;
+      sb[q] = d >= 1.0f ? 255 : d <= 0.0f ? 0 : min((int)(d * 256.0f), 255);
+      if (tid + q * 1024 < n) atomicAdd((unsigned long long*)&sub[sb[q]], (unsigned long long)exp_fix44(lv[q] - m));
     }
     __syncthreads();
-    const Pred all = {0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
-    auto mass = [m](int, float l) { return exp_fix44(l - m); };
-    cstar = radix_select<ORD_P, true>(CandSource{lv, li, n}, all, mass, target, esm);
+    if (tid < 64) {
+      // four sub-bins per lane, in order
+      uint64_t w4[4], t = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        w4[q] = sub[tid * 4 + q];
+        t += w4[q];
+      }
+      const uint64_t incl = wscan_incl_u64(t);
+      uint64_t c = incl - t;
+      if (c < target && target <= incl) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (c < target && target <= c + w4[q]) {
+            s_star = tid * 4 + q;
+            s_rem = target - c;
+          }
+          c += w4[q];
+        }
+      }
+    }
+    __syncthreads();
+    const int star = s_star;
+    const uint64_t t2 = s_rem;
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) {
+      if (tid + q * 1024 < n && sb[q] == star) {
+        const int slot = atomicAdd(&s_cnt, 1);
+        if (slot < WX_RANK) {
+          lc[slot] = comp_p(fkey(lv[q]), li[q]);
+          lw[slot] = exp_fix44(lv[q] - m);
+        }
+      }
+    }
+    __syncthreads();
+    const int ns = s_cnt;
+    if (ns <= WX_RANK) {
+      if (tid < ns) {
+        const uint64_t myc = lc[tid], myw = lw[tid];
+        uint64_t incl = 0;
+        for (int k = 0; k < ns; ++k) incl += lc[k] >= myc ? lw[k] : 0;
+        if (incl - myw < t2 && t2 <= incl) esm.bcast64[0] = myc;
+      }
+      __syncthreads();
+      cstar = esm.bcast64[0];
+    } else {
+      float* lvs = (float*)dyn;
+      int* lis = (int*)(dyn + WX_CAP * sizeof(float));
+      __syncthreads();
+      for (int j = tid; j < n; j += blockDim.x) {
+        lvs[j] = P.list_v[(size_t)b * WX_CAP + j];
+        lis[j] = P.list_i[(size_t)b * WX_CAP + j];
+      }
+      __syncthreads();
+      const Pred all = {0, 0, 0, 0, 0, 0, 0.0f, -INFINITY};
+      auto mass = [m](int, float l) { return exp_fix44(l - m); };
+      cstar = radix_select<ORD_P, true>(CandSource{lvs, lis, n}, all, mass, target, esm);
+    }
   }
   if (tid == 0) {
     rec->cstar = cstar;
