@@ -161,3 +161,36 @@ def test_wide_list_overflow_falls_back_exact(dev, oracle):
     assert sampling.last_paths(dev, B).cpu().numpy().tolist() == [1, 1]
     assert np.array_equal(kept.cpu().numpy(), ok)
     assert np.array_equal(tok.cpu().numpy(), ot)
+
+
+@pytest.mark.parametrize("tied,lead", [(3000, 100), (300, 20), (900, 0)])
+def test_wide_boundary_sub_bins(dev, oracle, tied, lead):
+    """Boundary lists above 64 entries go through 256 sub-bins of the
+    boundary bin: `tied` equal values with the cut among them (more than
+    1024 in one sub-bin takes the radix select), `lead` values above them,
+    and values near the tied one in the same bin but other sub-bins."""
+    from whallm_amd import sampling
+
+    rng = np.random.default_rng(tied + lead)
+    B, V = 3, 40000
+    x = np.full((B, V), -40.0, np.float32)
+    for b in range(B):
+        ids = rng.permutation(V)
+        x[b, ids[:lead]] = 5.0
+        x[b, ids[lead:lead + tied]] = 2.0
+        # neighbours inside the same 1/64-nat bin, in other sub-bins
+        x[b, ids[lead + tied:lead + tied + 200]] = 2.0 - rng.uniform(0.0, 0.0155, 200).astype(np.float32)
+    u = np.array([0.0, 0.5, 0.999], np.float32)
+    mass_lead = lead * 1.0
+    mass_tied = tied * np.exp(-3.0) if lead else tied * 1.0
+    top_p = float((mass_lead + 0.5 * mass_tied) / (mass_lead + mass_tied + 200 * np.exp(-3.0)))
+    for chain in (0, 1):
+        p = oracle.make_params(B, temperature=0.7, top_p=top_p, chain=chain)
+        ot, ok = oracle.sample(x, p, u)
+        announce(f"wide engine sub-bins tied={tied} lead={lead} chain={chain} p={top_p:.4f}")
+        tok, kept = sampling.sample(torch.from_numpy(x).to(dev), temperature=0.7, top_p=top_p,
+                                    chain="mlx" if chain == 0 else "whallm", uniforms=torch.from_numpy(u).to(dev),
+                                    return_kept=True)
+        assert np.all(sampling.last_paths(dev, B).cpu().numpy() == 6)
+        assert np.array_equal(kept.cpu().numpy(), ok)
+        assert np.array_equal(tok.cpu().numpy(), ot)
