@@ -337,7 +337,10 @@ def summarize_profile(workload: int, out: str, lmhead: str | None = None):
         f = sum(bf[k]) / len(bf[k])
         w = sum(bw[k]) / len(bw[k])
         b = (f * fscale + w * wscale) * 1024
-        tot += b
+        # the LM head's figure is its logits kernel alone: the bench also runs
+        # the greedy and sampled entry points, whose kernels read the weights too
+        if not lmhead or "lmhead_logits_kernel" in k:
+            tot += b
         rows.append((k.split("(")[0].replace("void ", ""), len(bf[k]), f, w, f * fscale * 1024, w * wscale * 1024))
     stats = list(csv.DictReader(open(glob.glob(os.path.join(out, "trace", "**", "*kernel_stats.csv"), recursive=True)[0])))
     bench, tr = last_json("bench.json"), last_json("trace.json")
@@ -373,7 +376,8 @@ def summarize_profile(workload: int, out: str, lmhead: str | None = None):
                   f"| {float(r['MinNs']) / 1000:.2f} | {float(r['MaxNs']) / 1000:.2f} |")
     if lmhead:
         md.append("\nThe bench calls each entry point in turn (the logits kernel; the greedy kernel and its "
-                  "per-row reduction).")
+                  "per-row reduction; the sampled entry point: the product with slice maxima, then the wide "
+                  "engine's wx_* kernels).")
     md.append(f"\nSum of the kernels' averages: {ksum:.2f} us{' (both entry points)' if lmhead else ' per call'}.  "
               f"The bench without the profiler measured "
               f"{bench['roofline']['kernel_avg_us']:.2f} us per call with HIP events on the launch stream (every kernel "
