@@ -39,8 +39,11 @@ def _inputs(dev, M, K, V, seed):
     return x, w
 
 
+# V = 129,280 and 131,000 take 8-wave workgroups at M <= 32 (their grids
+# spread evenly over the CUs), 131,000 with a part-filled last workgroup;
+# the others take 4 waves, or two x row blocks at M > 32
 @pytest.mark.parametrize("M,K,V", [(1, 256, 1000), (7, 2560, 151936), (33, 512, 5003), (64, 2560, 151936),
-                                   (16, 4096, 129280), (32, 64, 129)])
+                                   (16, 4096, 129280), (32, 64, 129), (3, 512, 131000), (32, 256, 131000)])
 def test_lm_head_logits_and_greedy(dev, oracle, M, K, V):
     from whallm_amd.lmhead import lm_head, lm_head_greedy
 
@@ -111,7 +114,8 @@ def test_lm_head_rejects(dev):
                 torch.zeros(10, 128, device=dev, dtype=torch.bfloat16))
 
 
-@pytest.mark.parametrize("M,K,V", [(1, 2560, 151936), (16, 1024, 129280), (64, 2560, 151936), (33, 512, 5003)])
+@pytest.mark.parametrize("M,K,V", [(1, 2560, 151936), (16, 1024, 129280), (64, 2560, 151936), (33, 512, 5003),
+                                   (5, 512, 131000)])
 def test_lm_head_sample_fused_wide(dev, oracle, M, K, V):
     """Rows filtered by top-p alone (or not at all): the product emits the
     sampler's slice maxima.  Tokens equal lm_head() then sample(), and the

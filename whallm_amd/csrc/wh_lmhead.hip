@@ -21,15 +21,18 @@
 //     fragments come from LDS, so every W byte crosses HBM once;
 //   * x is re-read from L2 by every workgroup, so with two x row blocks the
 //     workgroup is 8 waves (256 rows: half the x traffic of 4 waves); with
-//     one block, 4 waves (more workgroups, better balance).
+//     one block, 8 waves when that grid spreads evenly over the CUs, else 4
+//     (more workgroups, better balance).
 // (Loading MFMA fragments straight from memory -- 32 rows per load
 // instruction -- ran at 1.1-2.1 TB/s; the staged form at 3.4-6.5 TB/s.)
 // Epilogues: (a) the float32 logits, (b) greedy: per row the largest
-// (value, lowest index) key of the workgroup's 128 columns, written to a
+// (value, lowest index) key of the workgroup's 128 or 256 columns, written to a
 // partials buffer; wh_lmhead_greedy's second kernel reduces them per row.
 // The logits never reach HBM on the greedy path, and the two epilogues see
 // identical accumulator values, so the fused tokens equal the argmax of the
 // unfused logits.
+#include <atomic>
+
 #include "wh_internal.h"
 #include "wh_common.h"
 
@@ -282,6 +285,35 @@ static int lm_check(const wh_lmhead_args* a) {
 // greedy partials are sized for the narrowest workgroup.
 static int lm_blocks(int V, int cols) { return (V + cols - 1) / cols; }
 
+// Compute units of the current device, read once per device.
+static int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Waves per workgroup with one x row block (M <= 32).  The grid is a few
+// workgroups per CU, all streaming W at once; a workgroup count that leaves
+// the last round on the CUs part-filled lets some CUs run on alone.  Eight
+// waves (256 vocabulary rows, half the x re-reads per W byte of four) when
+// their grid fills at least 95 % of its rounds, else four (twice as many,
+// finer workgroups).  Measured on 256 CUs at K = 2560-7168: V = 129,280
+// (505 workgroups of 8 waves: 99 % of two rounds) runs 4-13 % faster on 8
+// waves; V = 151,936 (594: 77 % of three) 7-15 % slower, so it keeps 4
+// (1,187: 93 % of five).
+static int lm_waves_one_block(int V) {
+  const int cu = device_cus();
+  const int n = lm_blocks(V, 256);
+  const int rounds = (n + cu - 1) / cu;
+  return (double)n >= 0.95 * rounds * cu ? 8 : 4;
+}
+
 }  // namespace wh
 
 using namespace wh;
@@ -296,8 +328,11 @@ extern "C" int wh_lmhead_logits(const wh_lmhead_args* a, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   const char *x = (const char*)a->x, *w = (const char*)a->weight;
   const long long ldo = a->logits_stride;
-  // one x row block: 4 waves (128 rows); two: 8 waves (256 rows)
-  if (a->M <= 32)
+  // one x row block: 4 or 8 waves (128 or 256 rows); two: 8 waves
+  if (a->M <= 32 && lm_waves_one_block(a->V) == 8)
+    hipLaunchKernelGGL((lmhead_logits_kernel<1, LM_KS, 8>), dim3(lm_blocks(a->V, 256)), dim3(512), 0, st, x, w,
+                       a->logits_out, ldo, a->M, a->K, a->V);
+  else if (a->M <= 32)
     hipLaunchKernelGGL((lmhead_logits_kernel<1, LM_KS, 4>), dim3(lm_blocks(a->V, 128)), dim3(256), 0, st, x, w,
                        a->logits_out, ldo, a->M, a->K, a->V);
   else
@@ -327,7 +362,10 @@ extern "C" int wh_lmhead_greedy(const wh_lmhead_args* a, void* stream) {
   uint64_t* part = (uint64_t*)a->workspace;
   const char *x = (const char*)a->x, *w = (const char*)a->weight;
   int nwg;
-  if (a->M <= 32) {
+  if (a->M <= 32 && lm_waves_one_block(a->V) == 8) {
+    nwg = lm_blocks(a->V, 256);
+    hipLaunchKernelGGL((lmhead_greedy_kernel<1, LM_KS, 8>), dim3(nwg), dim3(512), 0, st, x, w, part, a->M, a->K, a->V);
+  } else if (a->M <= 32) {
     nwg = lm_blocks(a->V, 128);
     hipLaunchKernelGGL((lmhead_greedy_kernel<1, LM_KS, 4>), dim3(nwg), dim3(256), 0, st, x, w, part, a->M, a->K, a->V);
   } else {
@@ -376,7 +414,10 @@ extern "C" int wh_lmhead_sample(const wh_lmhead_args* lm, const wh_sample_args* 
   if (rc) return rc;
   const char *x = (const char*)lm->x, *w = (const char*)lm->weight;
   const long long ldo = lm->logits_stride;
-  if (lm->M <= 32)
+  if (lm->M <= 32 && lm_waves_one_block(lm->V) == 8)
+    hipLaunchKernelGGL((lmhead_slicemax_kernel<1, LM_KS, 8>), dim3(lm_blocks(lm->V, 256)), dim3(512), 0, st, x, w,
+                       lm->logits_out, ldo, lm->M, lm->K, lm->V, keys, G, SL);
+  else if (lm->M <= 32)
     hipLaunchKernelGGL((lmhead_slicemax_kernel<1, LM_KS, 4>), dim3(lm_blocks(lm->V, 128)), dim3(256), 0, st, x, w,
                        lm->logits_out, ldo, lm->M, lm->K, lm->V, keys, G, SL);
   else
