@@ -480,7 +480,10 @@ __global__ void __launch_bounds__(1024) wx_resolve_kernel(SampleKArgs a, WxPtrs 
     __shared__ int s_cnt, s_star;
     __shared__ uint64_t s_rem;
     if (tid < 256) sub[tid] = 0;
-    if (tid == 0) s_cnt = 0;
+    if (tid == 0) {
+      s_cnt = 0;
+      s_star = -1;
+    }
     __syncthreads();
     constexpr int LPT = WX_CAP / 1024;  // entries per thread at most
     float lv[LPT];
@@ -534,7 +537,10 @@ __global__ void __launch_bounds__(1024) wx_resolve_kernel(SampleKArgs a, WxPtrs 
     }
     __syncthreads();
     const int ns = s_cnt;
-    if (ns <= WX_RANK) {
+    // (the target lies within the list's mass, the sum of the same integer
+    // masses, so some sub-bin holds it; should none, the select below
+    // decides from the whole list)
+    if (star >= 0 && ns <= WX_RANK) {
       if (tid < ns) {
         const uint64_t myc = lc[tid], myw = lw[tid];
         uint64_t incl = 0;
