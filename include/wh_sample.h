@@ -94,7 +94,8 @@ extern "C" {
 #define WH_LMHEAD_MAX_ROWS 64    /* M of the LM-head entry points */
 
 typedef struct wh_sample_args {
-  const void* logits;        /* device, B rows of V values (dtype), row stride in elements */
+  const void* logits;        /* device, B rows of V values (dtype), row stride in elements;
+                                no NaN (entries may be -inf) */
   int32_t dtype;             /* WH_DTYPE_F32 or WH_DTYPE_BF16 (widened exactly to float32) */
   int32_t B;
   int32_t V;

@@ -64,6 +64,7 @@ CASES = [
     (17, 4097, "flat", 1, 1.0, 0.999, "f32"),
     (2, 262144, "flat", 0, 0.9, 0.98, "f32"),
     (64, 151936, "flat", 0, 1.0, 0.9, "bf16"),
+    (12, 129280, "quant", 0, 0.9, 0.95, "f32"),
 ]
 
 
@@ -194,3 +195,45 @@ def test_wide_boundary_sub_bins(dev, oracle, tied, lead):
         assert np.all(sampling.last_paths(dev, B).cpu().numpy() == 6)
         assert np.array_equal(kept.cpu().numpy(), ok)
         assert np.array_equal(tok.cpu().numpy(), ot)
+
+
+@pytest.mark.parametrize("B,dtype", [(3, "f32"), (3, "bf16"), (12, "f32"), (12, "bf16")])
+def test_wide_load_layouts_agree(dev, oracle, B, dtype):
+    """Rows the vector loads read (V a multiple of 4, rows aligned to four
+    entries) and the same rows as an offset view of a wider tensor (base and
+    row stride off that alignment: the per-entry loads).  Tokens, kept
+    counts and logprob rows equal the oracle's both ways, and the masked rows
+    agree between the two."""
+    from whallm_amd import sampling
+    from whallm_amd.synth import bf16_bits_to_f32, f32_to_bf16_bits
+
+    V = 40000
+    rng = np.random.default_rng(B * 31 + len(dtype))
+    x = _rows(rng, B, V, "peaky")
+    u = rng.random(B, dtype=np.float32)
+    if dtype == "bf16":
+        bits = f32_to_bf16_bits(x)
+        x = bf16_bits_to_f32(bits)
+        dense = torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        dense = torch.from_numpy(x).to(dev)
+    wide = torch.zeros(B, V + 3, device=dev, dtype=dense.dtype)
+    wide[:, 1:V + 1] = dense
+    view = wide[:, 1:V + 1]
+    kw = dict(temperature=0.8, top_p=0.9)
+    p = oracle.make_params(B, chain=1, **kw)
+    ot, ok, orow = oracle.sample(x, p, u, want_rows=True)
+    masked = []
+    for name, xt in (("vector", dense), ("per-entry", view)):
+        announce(f"wide engine load layout {name} B={B} {dtype}")
+        tok, rows, kept = sampling.sample(xt, uniforms=torch.from_numpy(u).to(dev), return_logprobs=True,
+                                          return_kept=True, chain="whallm", **kw)
+        paths = sampling.last_paths(dev, B).cpu().numpy()
+        assert np.all(np.isin(paths, (6, 1))), (name, paths)
+        assert np.array_equal(kept.cpu().numpy(), ok), name
+        assert np.array_equal(tok.cpu().numpy(), ot), name
+        _check_rows(rows.cpu().numpy(), orow)
+        masked.append(sampling.filter_rows(xt, chain="mlx", temperature=1.0, top_p=0.95, out_mode=1).cpu().numpy())
+    assert np.array_equal(masked[0], masked[1])
+    fin = np.isfinite(masked[0])
+    assert np.array_equal(masked[0][fin], x[fin])

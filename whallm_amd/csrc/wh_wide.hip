@@ -45,7 +45,8 @@ constexpr int WX_T = 256;       // threads per slice workgroup
 constexpr int WX_BINS = 2048;   // mass bins, 1/64 nat each, below the row max
 constexpr int WX_CAP = 8192;    // boundary-bin list capacity per row
 constexpr int WX_RANK = 1024;   // sub-bin lists up to this long are ranked directly
-constexpr int WX_DIRECT = 64;   // boundary lists up to this long are ranked without sub-bins
+constexpr int WX_DIRECT = 64;
+constexpr int WX_HS = 4;        // slices per histogram workgroup   // boundary lists up to this long are ranked without sub-bins
 constexpr int WX_MAXG = 256;    // slices per row, at most (V <= 2^18, 1024-entry slices)
 constexpr int WX_DONE = 1;      // WxRec.flags: token, count and row already written
 constexpr int WX_NONE = 2;      // WxRec.flags: nothing kept (set by the collect step)
@@ -116,25 +117,73 @@ __device__ __forceinline__ void wx_pen_table(const SampleKArgs& a, int b, int lo
   }
 }
 
-// A thread's E raw entries of the slice, ids lo + tid + 256 j (coalesced).
+// Id of a thread's entry j in the slice starting at lo.  Scalar layout:
+// lo + tid + 256 j, one 2- or 4-byte load per entry.  Vector layout (V a
+// multiple of 4, rows aligned to 4 entries): runs of four consecutive ids,
+// lo + 4 (tid + 256 (j / 4)) + j % 4, one 8- or 16-byte load per run, so a
+// wave's load instruction moves 512 or 1024 bytes instead of 128 or 256.
+// Either way the ids grow with j.
+// (The thread index within the slice's 256: a workgroup may cover several
+// slices, 256 threads each.)
+__device__ __forceinline__ int wx_t() { return (int)threadIdx.x & (WX_T - 1); }
+template <bool VEC>
+__device__ __forceinline__ int wx_id(int lo, int j) {
+  return VEC ? lo + 4 * (wx_t() + WX_T * (j >> 2)) + (j & 3) : lo + wx_t() + WX_T * j;
+}
+
+// A thread's E raw entries of the slice (coalesced, in the layout above).
 // Every load is unconditional, from an in-bounds address (entries past hi
 // read entry lo and become 0), with the element type chosen once outside
-// the loop: the E loads then issue back to back and are waited for once.
+// the loop: the loads then issue back to back and are waited for once.
 // (Conditional loads had compiled to one branch and one full wait per
 // entry, E dependent round trips per thread in every step of the engine.)
-template <int E>
+template <int E, bool VEC>
 __device__ __forceinline__ void wx_raw(const RowCtx& rc, int lo, int hi, float (&v)[E]) {
-  if (rc.xf) {
+  static_assert(!VEC || E % 4 == 0, "whole runs of four entries");
+  if (VEC) {
+    // a run lies wholly inside or outside [lo, hi): lo, hi and V are
+    // multiples of 4
+    constexpr int NQ = E / 4;
+    if (rc.xf) {
+      float4 q[NQ];
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        const int i0 = wx_id<true>(lo, 4 * g);
+        q[g] = *(const float4*)(rc.xf + (i0 < hi ? i0 : lo));
+      }
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        v[4 * g] = q[g].x;
+        v[4 * g + 1] = q[g].y;
+        v[4 * g + 2] = q[g].z;
+        v[4 * g + 3] = q[g].w;
+      }
+    } else {
+      uint2 q[NQ];
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        const int i0 = wx_id<true>(lo, 4 * g);
+        q[g] = *(const uint2*)(rc.xb + (i0 < hi ? i0 : lo));
+      }
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        v[4 * g] = bf16_to_f32((uint16_t)(q[g].x & 0xFFFFu));
+        v[4 * g + 1] = bf16_to_f32((uint16_t)(q[g].x >> 16));
+        v[4 * g + 2] = bf16_to_f32((uint16_t)(q[g].y & 0xFFFFu));
+        v[4 * g + 3] = bf16_to_f32((uint16_t)(q[g].y >> 16));
+      }
+    }
+  } else if (rc.xf) {
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-      const int i = lo + threadIdx.x + WX_T * j;
+      const int i = wx_id<false>(lo, j);
       v[j] = rc.xf[i < hi ? i : lo];
     }
   } else {
     uint16_t h[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-      const int i = lo + threadIdx.x + WX_T * j;
+      const int i = wx_id<false>(lo, j);
       h[j] = rc.xb[i < hi ? i : lo];
     }
 #pragma unroll
@@ -142,14 +191,41 @@ __device__ __forceinline__ void wx_raw(const RowCtx& rc, int lo, int hi, float (
   }
 #pragma unroll
   for (int j = 0; j < E; ++j)
-    if (lo + (int)threadIdx.x + WX_T * j >= hi) v[j] = 0.0f;
+    if (wx_id<VEC>(lo, j) >= hi) v[j] = 0.0f;
 }
 // A thread's E consecutive raw entries s0 .. s0 + E - 1 (the pick step's
-// layout), loaded the same way: unconditional, in bounds, back to back.
-template <int E>
+// layout), loaded the same way: unconditional, in bounds, back to back; in
+// runs of four with the vector layout's alignment (a run past hi reads the
+// slice's last run and becomes 0).
+template <int E, bool VEC>
 __device__ __forceinline__ void wx_raw_run(const RowCtx& rc, int s0, int hi, float (&v)[E]) {
   const int last = hi - 1;  // the slice is never empty
-  if (rc.xf) {
+  if (VEC) {
+    constexpr int NQ = E / 4;
+    if (rc.xf) {
+      float4 q[NQ];
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) q[g] = *(const float4*)(rc.xf + min(s0 + 4 * g, hi - 4));
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        v[4 * g] = q[g].x;
+        v[4 * g + 1] = q[g].y;
+        v[4 * g + 2] = q[g].z;
+        v[4 * g + 3] = q[g].w;
+      }
+    } else {
+      uint2 q[NQ];
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) q[g] = *(const uint2*)(rc.xb + min(s0 + 4 * g, hi - 4));
+#pragma unroll
+      for (int g = 0; g < NQ; ++g) {
+        v[4 * g] = bf16_to_f32((uint16_t)(q[g].x & 0xFFFFu));
+        v[4 * g + 1] = bf16_to_f32((uint16_t)(q[g].x >> 16));
+        v[4 * g + 2] = bf16_to_f32((uint16_t)(q[g].y & 0xFFFFu));
+        v[4 * g + 3] = bf16_to_f32((uint16_t)(q[g].y >> 16));
+      }
+    }
+  } else if (rc.xf) {
 #pragma unroll
     for (int j = 0; j < E; ++j) v[j] = rc.xf[min(s0 + j, last)];
   } else {
@@ -164,24 +240,24 @@ __device__ __forceinline__ void wx_raw_run(const RowCtx& rc, int s0, int hi, flo
     if (s0 + j >= hi) v[j] = 0.0f;
 }
 // Raw entries to effective (penalised, -0 as +0) values.
-template <int E>
+template <int E, bool VEC>
 __device__ __forceinline__ void wx_pen(const RowCtx& rc, int lo, int hi, float (&v)[E]) {
 #pragma unroll
   for (int j = 0; j < E; ++j) {
-    const int i = lo + threadIdx.x + WX_T * j;
+    const int i = wx_id<VEC>(lo, j);
     v[j] = i < hi ? rc.val_from(i, v[j]) : 0.0f;
   }
 }
 
 // The slice's effective values: the logits loads issue first, then the
 // penalty table is built while they are in flight.
-template <int E>
+template <int E, bool VEC>
 __device__ __forceinline__ void wx_slice(const SampleKArgs& a, int b, int lo, int hi, char* dyn, RowCtx& rc,
                                          float (&v)[E]) {
   wx_ptrs(a, b, rc);
-  wx_raw<E>(rc, lo, hi, v);
+  wx_raw<E, VEC>(rc, lo, hi, v);
   wx_pen_table(a, b, lo, hi, dyn, rc);
-  wx_pen<E>(rc, lo, hi, v);
+  wx_pen<E, VEC>(rc, lo, hi, v);
 }
 
 // Row max from the slice maxima (every thread returns it).
@@ -217,7 +293,7 @@ __device__ __forceinline__ int wx_bin(float m, float l) {
   return d >= 32.0f ? WX_BINS - 1 : (int)(d * 64.0f);
 }
 
-template <int E>
+template <int E, bool VEC>
 __global__ void __launch_bounds__(WX_T) wx_max_kernel(SampleKArgs a, WxPtrs P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ float sf[16];
@@ -226,14 +302,14 @@ __global__ void __launch_bounds__(WX_T) wx_max_kernel(SampleKArgs a, WxPtrs P) {
   const int lo = g * P.SL, hi = min(a.V, lo + P.SL);
   RowCtx rc;
   float v[E];
-  wx_slice<E>(a, b, lo, hi, dyn, rc, v);
+  wx_slice<E, VEC>(a, b, lo, hi, dyn, rc, v);
   const WxRow rp = wx_row(a, b);
   float* out = (a.out_rows && rp.greedy) ? a.out_rows + (long long)b * a.V : nullptr;
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
 #pragma unroll
   for (int j = 0; j < E; ++j) {
-    const int i = lo + tid + WX_T * j;
+    const int i = wx_id<VEC>(lo, j);
     if (i >= hi) break;
     if (bi == 0x7FFFFFFF || v[j] > bv) {
       bv = v[j];
@@ -258,38 +334,47 @@ __global__ void __launch_bounds__(WX_T) wx_max_kernel(SampleKArgs a, WxPtrs P) {
   }
 }
 
-template <int E>
-__global__ void __launch_bounds__(WX_T) wx_hist_kernel(SampleKArgs a, WxPtrs P) {
+// The histogram step: one workgroup of 256 WX_HS threads per WX_HS
+// consecutive slices (256 threads each), one LDS histogram for all of them,
+// so each non-empty bin costs one global atomic per WX_HS slices.  (With one
+// slice per workgroup the global atomics took half the step: 31 against
+// 15.5 us at B = 64, V = 151,936.)  Slices past the row's last read the
+// workgroup's first slice over an empty range: in bounds, nothing counted.
+template <int E, bool VEC>
+__global__ void __launch_bounds__(WX_T * WX_HS) wx_hist_kernel(SampleKArgs a, WxPtrs P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ float sf[16];
   __shared__ uint64_t hw[WX_BINS];
-  const int b = blockIdx.y, g = blockIdx.x, tid = threadIdx.x;
+  const int b = blockIdx.y, tid = threadIdx.x;
   const WxRow rp = wx_row(a, b);
   if (rp.greedy || !rp.use_p) return;
-  const int lo = g * P.SL, hi = min(a.V, lo + P.SL);
+  const int s0 = blockIdx.x * WX_HS, sl = s0 + (tid >> 8);
+  const bool has = sl < P.G;
+  const int lo = (has ? sl : s0) * P.SL, hi = has ? min(a.V, lo + P.SL) : lo;
+  const int wlo = s0 * P.SL, whi = min(a.V, (s0 + WX_HS) * P.SL);  // the workgroup's id range
   RowCtx rc;
   float v[E];
   wx_ptrs(a, b, rc);
-  wx_raw<E>(rc, lo, hi, v);  // in flight with the slice maxima
+  wx_raw<E, VEC>(rc, lo, hi, v);  // in flight with the slice maxima
   const float m = wx_row_max(P, b, sf);
   if (m == -INFINITY) return;
-  for (int j = tid; j < WX_BINS; j += WX_T) hw[j] = 0;
+  for (int j = tid; j < WX_BINS; j += WX_T * WX_HS) hw[j] = 0;
   __syncthreads();
-  wx_pen_table(a, b, lo, hi, dyn, rc);
-  wx_pen<E>(rc, lo, hi, v);
+  wx_pen_table(a, b, wlo, whi, dyn, rc);
+  wx_pen<E, VEC>(rc, lo, hi, v);
 #pragma unroll
   for (int j = 0; j < E; ++j) {
     const float l = v[j];
-    if (lo + tid + WX_T * j >= hi || l != l) continue;
+    if (wx_id<VEC>(lo, j) >= hi || l != l) continue;
     const uint64_t w = exp_fix44(l - m);
     if (w) atomicAdd((unsigned long long*)&hw[wx_bin(m, l)], (unsigned long long)w);
   }
   __syncthreads();
-  for (int j = tid; j < WX_BINS; j += WX_T)
+  for (int j = tid; j < WX_BINS; j += WX_T * WX_HS)
     if (hw[j]) atomicAdd((unsigned long long*)&P.hist_w[(size_t)b * WX_BINS + j], (unsigned long long)hw[j]);
 }
 
-template <int E>
+template <int E, bool VEC>
 __global__ void __launch_bounds__(WX_T) wx_collect_kernel(SampleKArgs a, WxPtrs P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ float sf[16];
@@ -297,17 +382,18 @@ __global__ void __launch_bounds__(WX_T) wx_collect_kernel(SampleKArgs a, WxPtrs 
   __shared__ uint64_t bc[1];
   __shared__ int bs[2];
   const int b = blockIdx.y, g = blockIdx.x, tid = threadIdx.x;
+  const bool first = g == 0 && tid == 0;  // writes the row's record
   const WxRow rp = wx_row(a, b);
   if (rp.greedy || !rp.use_p) return;
   const int lo = g * P.SL, hi = min(a.V, lo + P.SL);
   RowCtx rc;
   float v[E];
   wx_ptrs(a, b, rc);
-  wx_raw<E>(rc, lo, hi, v);  // in flight with the maxima and the histogram
+  wx_raw<E, VEC>(rc, lo, hi, v);  // in flight with the maxima and the histogram
   const float m = wx_row_max(P, b, sf);
   WxRec* rec = P.rec + b;
   if (m == -INFINITY) {  // nothing kept
-    if (g == 0 && tid == 0) rec->flags = WX_NONE;
+    if (first) rec->flags = WX_NONE;
     return;
   }
   // the boundary bin, from the row's whole histogram (every workgroup alike)
@@ -323,7 +409,7 @@ __global__ void __launch_bounds__(WX_T) wx_collect_kernel(SampleKArgs a, WxPtrs 
   const uint64_t excl = block_exclusive_scan_u64(ls, s64, &Z);
   const uint64_t F = floor_theta_z(rp.theta, Z);
   if (Z <= F) {  // nothing kept
-    if (g == 0 && tid == 0) rec->flags = WX_NONE;
+    if (first) rec->flags = WX_NONE;
     return;
   }
   const uint64_t R = Z - F;
@@ -340,19 +426,19 @@ __global__ void __launch_bounds__(WX_T) wx_collect_kernel(SampleKArgs a, WxPtrs 
   }
   __syncthreads();
   const int bstar = bs[0];
-  if (g == 0 && tid == 0) {
+  if (first) {
     rec->cum_excl = bc[0];
     rec->R = R;
     rec->bstar = bstar;
     rec->flags = 0;
   }
   wx_pen_table(a, b, lo, hi, dyn, rc);
-  wx_pen<E>(rc, lo, hi, v);
+  wx_pen<E, VEC>(rc, lo, hi, v);
   // the slice's boundary-bin entries: one list reservation per workgroup
   uint32_t hit = 0;
 #pragma unroll
   for (int j = 0; j < E; ++j) {
-    const int i = lo + tid + WX_T * j;
+    const int i = wx_id<VEC>(lo, j);
     if (i < hi && v[j] == v[j] && wx_bin(m, v[j]) == bstar) hit |= 1u << j;
   }
   uint64_t nall;
@@ -366,7 +452,7 @@ __global__ void __launch_bounds__(WX_T) wx_collect_kernel(SampleKArgs a, WxPtrs 
     if (!((hit >> j) & 1u)) continue;
     if (slot < WX_CAP) {
       P.list_v[(size_t)b * WX_CAP + slot] = v[j];
-      P.list_i[(size_t)b * WX_CAP + slot] = lo + tid + WX_T * j;
+      P.list_i[(size_t)b * WX_CAP + slot] = wx_id<VEC>(lo, j);
     }
     ++slot;
   }
@@ -574,7 +660,7 @@ __device__ __forceinline__ bool wx_keep(const WxRow& rp, const WxRec& r, int i, 
   return !rp.use_p || comp_p(fkey(l), i) >= r.cstar;
 }
 
-template <int E>
+template <int E, bool VEC>
 __global__ void __launch_bounds__(WX_T) wx_drawsum_kernel(SampleKArgs a, WxPtrs P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ float sf[16];
@@ -587,18 +673,39 @@ __global__ void __launch_bounds__(WX_T) wx_drawsum_kernel(SampleKArgs a, WxPtrs 
   RowCtx rc;
   float v[E];
   wx_ptrs(a, b, rc);
-  wx_raw<E>(rc, lo, hi, v);  // in flight with the record and the maxima
+  // the record and this slice's max first, then the logits: loads complete
+  // in order, so the test below waits for the first two alone
   const WxRec r = P.rec[b];
+  float smax;
+  if (P.part_key) {
+    const uint64_t k = P.part_key[(size_t)b * P.G + g];
+    smax = k ? key_to_float((uint32_t)(k >> 32)) : -INFINITY;
+  } else {
+    smax = P.part_m[(size_t)b * P.G + g];
+  }
+  asm volatile("" ::: "memory");
+  wx_raw<E, VEC>(rc, lo, hi, v);  // in flight with the maxima
   if (r.flags & WX_DONE) return;
+  float* out = (a.out_rows && a.out_mode == WH_OUT_MASKED) ? a.out_rows + (long long)b * a.V : nullptr;
+  // a slice whose largest (effective) value lies below the cut's value keeps
+  // nothing: every composite there is below cstar.  On peaked rows that is
+  // all slices but the nucleus's, whose passes this skips (not when the
+  // masked row is written: its -inf entries are this pass's).
+  if (rp.use_p && !out && fkey(smax + 0.0f) < (uint32_t)(r.cstar >> 18)) {
+    if (tid == 0) {
+      P.part_vw[(size_t)b * P.G + g] = 0;
+      P.part_n[(size_t)b * P.G + g] = 0;
+    }
+    return;
+  }
   const float m = wx_row_max(P, b, sf);
   wx_pen_table(a, b, lo, hi, dyn, rc);
-  wx_pen<E>(rc, lo, hi, v);
-  float* out = (a.out_rows && a.out_mode == WH_OUT_MASKED) ? a.out_rows + (long long)b * a.V : nullptr;
+  wx_pen<E, VEC>(rc, lo, hi, v);
   uint64_t s = 0;
   int cnt = 0;
 #pragma unroll
   for (int j = 0; j < E; ++j) {
-    const int i = lo + tid + WX_T * j;
+    const int i = wx_id<VEC>(lo, j);
     if (i >= hi) break;
     const bool k = wx_keep(rp, r, i, v[j]);
     if (k) {
@@ -615,7 +722,7 @@ __global__ void __launch_bounds__(WX_T) wx_drawsum_kernel(SampleKArgs a, WxPtrs 
   }
 }
 
-template <int E>
+template <int E, bool VEC>
 __global__ void __launch_bounds__(WX_T) wx_pick_kernel(SampleKArgs a, WxPtrs P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ float sf[16];
@@ -657,7 +764,7 @@ __global__ void __launch_bounds__(WX_T) wx_pick_kernel(SampleKArgs a, WxPtrs P) 
   // E consecutive ids per thread, so the block scan runs in id order
   const int s0 = lo + tid * E;
   float v[E];
-  wx_raw_run<E>(rc, s0, hi, v);
+  wx_raw_run<E, VEC>(rc, s0, hi, v);
   wx_pen_table(a, b, lo, hi, dyn, rc);
 #pragma unroll
   for (int j = 0; j < E; ++j) v[j] = s0 + j < hi ? rc.val_from(s0 + j, v[j]) : 0.0f;
@@ -684,7 +791,7 @@ __global__ void __launch_bounds__(WX_T) wx_pick_kernel(SampleKArgs a, WxPtrs P) 
   }
 }
 
-template <int E>
+template <int E, bool VEC>
 __global__ void __launch_bounds__(WX_T) wx_rows_kernel(SampleKArgs a, WxPtrs P) {
   extern __shared__ __align__(16) char dyn[];
   __shared__ float sf[16];
@@ -695,17 +802,17 @@ __global__ void __launch_bounds__(WX_T) wx_rows_kernel(SampleKArgs a, WxPtrs P) 
   RowCtx rc;
   float v[E];
   wx_ptrs(a, b, rc);
-  wx_raw<E>(rc, lo, hi, v);
+  wx_raw<E, VEC>(rc, lo, hi, v);
   const WxRec r = P.rec[b];
   if (r.flags & WX_DONE) return;
   const float m = wx_row_max(P, b, sf);
   wx_pen_table(a, b, lo, hi, dyn, rc);
-  wx_pen<E>(rc, lo, hi, v);
+  wx_pen<E, VEC>(rc, lo, hi, v);
   const double lz = log(ldexp((double)r.ZV, -44));
   float* out = a.out_rows + (long long)b * a.V;
 #pragma unroll
   for (int j = 0; j < E; ++j) {
-    const int i = lo + tid + WX_T * j;
+    const int i = wx_id<VEC>(lo, j);
     if (i >= hi) break;
     out[i] = wx_keep(rp, r, i, v[j]) ? (float)((double)chain_scale(a.chain, v[j] - m, rp.invT, rp.rTc) - lz)
                                      : -INFINITY;
@@ -762,32 +869,34 @@ static int wx_lds(const void* fn, size_t lds) {
   return WH_OK;
 }
 
-template <int E>
+template <int E, bool VEC>
 static int wx_launch(const SampleKArgs& k, WxPtrs P, hipStream_t st, bool from_keys) {
   const bool any_p = k.top_p_rows || (k.top_p > 0.0 && k.top_p < 1.0);
   // slice workgroups: the penalty table of one slice's id range
   const size_t lds_s = k.hcap > 0 ? (size_t)k.hcap * 12 + (size_t)(WX_T * E / 32) * 4 : 0;
+  const size_t lds_h = k.hcap > 0 ? (size_t)k.hcap * 12 + (size_t)(WX_T * E * WX_HS / 32) * 4 : 0;
   const size_t lds_r = std::max({penalty_lds_bytes(k), (size_t)WX_CAP * 8, (size_t)WX_RANK * 16});
   int rc;
-  if ((rc = wx_lds((const void*)wx_max_kernel<E>, lds_s)) || (rc = wx_lds((const void*)wx_hist_kernel<E>, lds_s)) ||
-      (rc = wx_lds((const void*)wx_collect_kernel<E>, lds_s)) || (rc = wx_lds((const void*)wx_resolve_kernel, lds_r)) ||
-      (rc = wx_lds((const void*)wx_drawsum_kernel<E>, lds_s)) || (rc = wx_lds((const void*)wx_pick_kernel<E>, lds_s)) ||
-      (rc = wx_lds((const void*)wx_rows_kernel<E>, lds_s)))
+  if ((rc = wx_lds((const void*)wx_max_kernel<E, VEC>, lds_s)) || (rc = wx_lds((const void*)wx_hist_kernel<E, VEC>, lds_h)) ||
+      (rc = wx_lds((const void*)wx_collect_kernel<E, VEC>, lds_s)) || (rc = wx_lds((const void*)wx_resolve_kernel, lds_r)) ||
+      (rc = wx_lds((const void*)wx_drawsum_kernel<E, VEC>, lds_s)) || (rc = wx_lds((const void*)wx_pick_kernel<E, VEC>, lds_s)) ||
+      (rc = wx_lds((const void*)wx_rows_kernel<E, VEC>, lds_s)))
     return rc;
   const dim3 gs(P.G, k.B);
-  if (!from_keys) hipLaunchKernelGGL(wx_max_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
+  if (!from_keys) hipLaunchKernelGGL((wx_max_kernel<E, VEC>), gs, dim3(WX_T), lds_s, st, k, P);
   if (any_p) {
-    hipLaunchKernelGGL(wx_hist_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
-    hipLaunchKernelGGL(wx_collect_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
+    hipLaunchKernelGGL((wx_hist_kernel<E, VEC>), dim3((P.G + WX_HS - 1) / WX_HS, k.B), dim3(WX_T * WX_HS), lds_h, st,
+                       k, P);
+    hipLaunchKernelGGL((wx_collect_kernel<E, VEC>), gs, dim3(WX_T), lds_s, st, k, P);
   }
   // the resolve step settles rows with top-p and greedy rows; without
   // either (a scalar temperature above 0 and no top-p) the max step's
   // records stand
   if (any_p || k.T_rows) hipLaunchKernelGGL(wx_resolve_kernel, dim3(k.B), dim3(1024), lds_r, st, k, P);
-  hipLaunchKernelGGL(wx_drawsum_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
-  hipLaunchKernelGGL(wx_pick_kernel<E>, dim3(k.B), dim3(WX_T), lds_s, st, k, P);
+  hipLaunchKernelGGL((wx_drawsum_kernel<E, VEC>), gs, dim3(WX_T), lds_s, st, k, P);
+  hipLaunchKernelGGL((wx_pick_kernel<E, VEC>), dim3(k.B), dim3(WX_T), lds_s, st, k, P);
   if (k.out_rows && k.out_mode == WH_OUT_LOGPROBS)
-    hipLaunchKernelGGL(wx_rows_kernel<E>, gs, dim3(WX_T), lds_s, st, k, P);
+    hipLaunchKernelGGL((wx_rows_kernel<E, VEC>), gs, dim3(WX_T), lds_s, st, k, P);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WH_EHIP, "wide engine launch failed: %s", hipGetErrorString(e));
   return WH_OK;
@@ -814,10 +923,25 @@ static WxPtrs wx_ptrs_of(const SampleKArgs& k, void* workspace) {
   return P;
 }
 
+// Rows the vector layout can read: V a multiple of 4 (a run of four ids lies
+// wholly inside or outside every slice), the logits and the row stride
+// aligned to one run (8 bytes in bfloat16, 16 in float32).
+static bool wx_vec(const SampleKArgs& k) {
+  const size_t esz = k.dtype == WH_DTYPE_BF16 ? 2 : 4;
+  return k.V % 4 == 0 && (uintptr_t)k.logits % (4 * esz) == 0 && ((size_t)k.row_stride * esz) % (4 * esz) == 0;
+}
+
+static int wx_dispatch(const SampleKArgs& k, WxPtrs P, hipStream_t st, bool from_keys) {
+  const bool vec = wx_vec(k);
+  if (P.SL == WX_T * 4)
+    return vec ? wx_launch<4, true>(k, P, st, from_keys) : wx_launch<4, false>(k, P, st, from_keys);
+  return vec ? wx_launch<16, true>(k, P, st, from_keys) : wx_launch<16, false>(k, P, st, from_keys);
+}
+
 int launch_sample_wide(const SampleKArgs& k, const wh_sample_args* p, hipStream_t st) {
   WxPtrs P = wx_ptrs_of(k, p->workspace);
   if (P.G > WX_MAXG) return fail(WH_ELIMIT, "too many slices for the wide engine");
-  return P.SL == WX_T * 4 ? wx_launch<4>(k, P, st, false) : wx_launch<16>(k, P, st, false);
+  return wx_dispatch(k, P, st, false);
 }
 
 // The wide engine after an LM head that writes the slice maxima: the keys'
@@ -839,7 +963,7 @@ int wide_keys_prepare(const SampleKArgs& k, void* workspace, hipStream_t st, uin
 int launch_sample_wide_from_keys(const SampleKArgs& k, const wh_sample_args* p, hipStream_t st) {
   WxPtrs P = wx_ptrs_of(k, p->workspace);
   P.part_key = (uint64_t*)((char*)p->workspace + wx_layout(k.B, k.V).part_key);
-  return P.SL == WX_T * 4 ? wx_launch<4>(k, P, st, true) : wx_launch<16>(k, P, st, true);
+  return wx_dispatch(k, P, st, true);
 }
 
 }  // namespace wh
