@@ -454,10 +454,11 @@ __global__ void __launch_bounds__(FT) slice_kernel(const char* __restrict__ logi
   // 8): the grid is (8 G, B / 8) and (x, y) takes slice x / 8 of row
   // 8 y + x % 8, so a row's G slices share one XCD's L2, which fetches the
   // row's history and parameters from HBM once, and the merge's workgroup b
-  // runs on XCD b % 8 as well (workload 2 -0.3 us, workload 5 -1.1 us,
-  // workload 4 -0.4 us).  Otherwise the grid is (G, B), a row's slices
-  // spread over the XCDs (a row count read in the kernel, to bound the
-  // mapped rows, had cost B = 1 0.2-0.5 us).
+  // runs on XCD b % 8 as well (B = 64, V = 151,936 bf16 with 2,048-id
+  // histories: -0.3 us per call; B = 128 with 4,096-id histories: -1.1 us;
+  // B = 256, V = 129,280 f32: -0.4 us).  Otherwise the grid is (G, B), a
+  // row's slices spread over the XCDs (a row count read in the kernel, to
+  // bound the mapped rows, had cost B = 1 0.2-0.5 us).
   const int b = XM ? 8 * (int)blockIdx.y + ((int)blockIdx.x & 7) : (int)blockIdx.y;
   const int s = XM ? (int)blockIdx.x >> 3 : (int)blockIdx.x;
   const int v0 = s * SL, v1 = min(V, v0 + SL);
@@ -1530,8 +1531,9 @@ __device__ __forceinline__ int block_finish(const SampleKArgs& a, int b, const R
 // the workgroup.  Returns the path code (4 done, 3 exact engine).  The
 // arguments are read in place from the kernel-argument segment (a pointer,
 // not a copy).  It is inlined: out of line, its LDS pointers arrive as
-// generic pointers and every LDS access becomes a flat access (workload 4
-// took 84.4 us per call that way, 79.2 us inlined).  hdl is the kernel's
+// generic pointers and every LDS access becomes a flat access (B = 256,
+// V = 129,280 f32 rows with per-row top-k up to 1024 took 84.4 us per call
+// that way, 79.2 us inlined).  hdl is the kernel's
 // register copy of the summaries (lane s < G holds slice s): the counts and
 // the normaliser bounds come from it, and the candidates are loaded U per
 // thread before any is stored, so a row costs one round trip per U * 512
