@@ -475,3 +475,40 @@ def test_confident_rows_with_penalties_settle(S, dev, oracle, dtype):
     assert np.array_equal(tok.cpu().numpy(), ot)
     assert not np.any((paths == 1) | (paths == 3)), paths
     assert np.any((paths == 7) | (paths == 8)), paths  # the second pass ran
+
+
+@pytest.mark.parametrize("B,dtype", [(8, "bf16"), (24, "f32"), (40, "bf16"), (7, "f32"), (9, "bf16")])
+def test_slice_placement_batches(S, dev, oracle, B, dtype):
+    """Batch sizes that are multiples of 8 run the slice grid that puts a
+    row's slices on one XCD (row 8 y + x % 8, slice x / 8); others run the
+    plain (slice, row) grid.  Per-row histories with all three penalties,
+    top-k, top-p and min-p: tokens and kept counts equal the oracle's on the
+    fast engine, for every row (a misplaced row or slice would read another
+    row's logits or history)."""
+    from whallm_amd import synth
+
+    rng = np.random.default_rng(900 + B)
+    V, H = 151936 if dtype == "bf16" else 129280, 512
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    x[np.arange(B), rng.integers(0, V, B)] += 9.0  # a distinct leader per row
+    hist = rng.integers(0, V, (B, H)).astype(np.int32)
+    hlen = rng.integers(H // 2, H + 1, B).astype(np.int32)
+    if dtype == "bf16":
+        bits = synth.f32_to_bf16_bits(x)
+        x = synth.bf16_bits_to_f32(bits)
+        xd = torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        xd = torch.from_numpy(x).to(dev)
+    u = rng.random(B, dtype=np.float32)
+    kw = dict(temperature=0.8, top_k=40, top_p=0.9, min_p=0.02, repetition_penalty=1.2, presence_penalty=0.4,
+              frequency_penalty=0.2, repetition_context=H, presence_context=64, frequency_context=H)
+    p = oracle.make_params(B, chain=1, **kw)
+    ot, ok = oracle.sample(x, p, u, hist, hlen)
+    announce(f"wh_sample slice placement B={B} {dtype}")
+    tok, kept = S.sample(xd, chain=1, history=torch.from_numpy(hist).to(dev),
+                         history_len=torch.from_numpy(hlen).to(dev), uniforms=torch.from_numpy(u).to(dev),
+                         return_kept=True, **kw)
+    paths = S.last_paths(dev, B).cpu().numpy()
+    assert not np.any((paths == 1) | (paths == 3)), paths
+    assert np.array_equal(kept.cpu().numpy(), ok)
+    assert np.array_equal(tok.cpu().numpy(), ot)
