@@ -237,3 +237,40 @@ def test_wide_load_layouts_agree(dev, oracle, B, dtype):
     assert np.array_equal(masked[0], masked[1])
     fin = np.isfinite(masked[0])
     assert np.array_equal(masked[0][fin], x[fin])
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_wide_penalties_long_slices(dev, oracle, dtype):
+    """B > 8 (4096-entry slices; the histogram step's workgroups build one
+    penalty table over four slices' ids): repetition, presence and frequency
+    penalties over per-row histories, top-p alone, both chains; tokens and
+    kept counts equal the oracle's."""
+    from whallm_amd import sampling
+    from whallm_amd.synth import bf16_bits_to_f32, f32_to_bf16_bits
+
+    rng = np.random.default_rng(4242 + len(dtype))
+    B, V, H = 12, 70000, 600
+    x = _rows(rng, B, V, "peaky")
+    hist = rng.integers(0, V, (B, H)).astype(np.int32)
+    hist[:, :40] = np.argsort(-x, axis=1)[:, :40]  # penalise the rows' leaders too
+    hlen = rng.integers(H // 2, H + 1, B).astype(np.int32)
+    if dtype == "bf16":
+        bits = f32_to_bf16_bits(x)
+        x = bf16_bits_to_f32(bits)
+        xt = torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        xt = torch.from_numpy(x).to(dev)
+    u = rng.random(B, dtype=np.float32)
+    pen = dict(repetition_penalty=1.3, presence_penalty=0.6, frequency_penalty=0.3, repetition_context=0,
+               presence_context=200, frequency_context=0)
+    for chain, T, top_p in ((0, 0.2, 0.98), (1, 0.9, 0.9)):
+        p = oracle.make_params(B, temperature=T, top_p=top_p, chain=chain, **pen)
+        ot, ok = oracle.sample(x, p, u, hist, hlen)
+        announce(f"wide engine penalties B={B} {dtype} chain={chain}")
+        tok, kept = sampling.sample(xt, temperature=T, top_p=top_p, chain="mlx" if chain == 0 else "whallm",
+                                    history=torch.from_numpy(hist).to(dev), history_len=torch.from_numpy(hlen).to(dev),
+                                    uniforms=torch.from_numpy(u).to(dev), return_kept=True, **pen)
+        paths = sampling.last_paths(dev, B).cpu().numpy()
+        assert np.all(np.isin(paths, (6, 1))), paths
+        assert np.array_equal(kept.cpu().numpy(), ok), chain
+        assert np.array_equal(tok.cpu().numpy(), ot), chain
